@@ -1,0 +1,298 @@
+"""Benchmark of the GDN decode / prefill paths on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Prints ONE JSON line.  The headline ``value`` is the decode step at B = 64
+(configuration 1): HBM GB/s on state traffic (state read + new_state write,
+2*64*8*128*128*4 B per step).  A "step" is one decode launch over the whole
+batch with all inputs already resident in HBM.  Timing: W untimed warmup
+steps, then exactly K steps bracketed by torch.cuda.synchronize(); the state
+buffers rotate over enough sets (> the 256 MiB Infinity Cache) that every step
+reads cold data.  The same line carries:
+
+* ``roofline`` for the decode kernel: algorithmic bytes per launch (state +
+  q, k, v, a, b, out) / mean launch duration from HIP events on the launch
+  stream, against the 8 TB/s HBM3E peak; ``traffic`` is the measured HBM
+  bytes per launch when a rocprofv3 counter summary exists in profiles/;
+* ``cpu_baseline``: the CPU restatement of the reference oracle (per-(b,h)
+  loop, the reference's structure) timed on this host on the same B = 64 step;
+* ``prefill``: configuration 3 (16 sequences, 16384 tokens) tokens/s with its
+  roofline (HBM, algorithmic bytes) and the oracle's CPU rate on a bounded
+  sample, plus configurations 2 and 4 and decode B = 1 as secondary figures.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBPS = 8000.0           # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0        # MI355X dense bf16 MFMA, published
+MALL_BYTES = 256 << 20
+NV, NQK, D = 8, 4, 128
+
+
+def decode_bytes(B: int) -> tuple[int, int]:
+    """(state bytes, total algorithmic bytes) of one decode step."""
+    state = 2 * B * NV * D * D * 4
+    other = B * (2 * NQK * D * 2 + NV * D * 2 + NV * D * 2 + 2 * NV * 2) + 2 * NV * 4
+    return state, state + other
+
+
+def prefill_bytes(T: int, N: int) -> int:
+    """Inputs read once + outputs written once (q, k, v, a, b, state in, o, new_state)."""
+    return (2 * T * NQK * D * 2 + T * NV * D * 2 + 2 * T * NV * 2 + 2 * NV * 4 +
+            N * NV * D * D * 4 + T * NV * D * 2 + N * NV * D * D * 4)
+
+
+def prefill_flops(lengths, chunk=64) -> float:
+    """Algorithmic FLOPs: per v-head per chunk of c tokens
+    6 c K V + c^2 (3K + 2V) + c^3 / 3."""
+    tot = 0.0
+    for L in lengths:
+        for c0 in range(0, L, chunk):
+            c = min(chunk, L - c0)
+            tot += 6 * c * D * D + c * c * (3 * D + 2 * D) + c ** 3 / 3
+    return NV * tot
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from profiles/<name> ('hbm_bytes_per_launch: N')."""
+    path = REPO / "profiles" / name
+    if not path.exists():
+        return None
+    m = re.search(r"hbm_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def time_launches(fn, sets, steps, warmup, torch):
+    """Warmup, then exactly `steps` launches rotating over `sets`; returns
+    (wall ms per step, mean event ms per launch)."""
+    for i in range(warmup):
+        fn(sets[i % len(sets)])
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        fn(sets[i % len(sets)])
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return wall_ms, statistics.mean(ev), statistics.median(ev)
+
+
+def hbm_copy_gbps(torch, dev, nbytes=1 << 30, reps=10):
+    """Achievable HBM bandwidth: device-to-device copy of `nbytes` (read + write)."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / reps
+    del src, dst
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def cpu_decode_baseline(torch, B=64, min_seconds=8.0):
+    from kachua_mlsys_amd.inputs import decode_inputs
+    from oracle.gdn_oracle import decode_ref
+
+    d = decode_inputs(B, seed=0)
+    times = []
+    t_end = time.perf_counter() + min_seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        decode_ref(*d.args())
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    state_b, _ = decode_bytes(B)
+    return {"value": round(state_b / t / 1e9, 4), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle decode_ref (per-(b,h) fp32 loop) on the full B={B} step, "
+                      f"median of {len(times)} runs, {t * 1e3:.1f} ms/step"}
+
+
+def cpu_prefill_baseline(torch, p, max_tokens=2048):
+    """Oracle prefill on the first sequences of the workload, up to max_tokens."""
+    from kachua_mlsys_amd.inputs import PrefillInputs
+    from oracle.gdn_oracle import prefill_ref
+
+    lengths = p.lengths
+    n, tot = 0, 0
+    while n < len(lengths) and tot + lengths[n] <= max_tokens:
+        tot += lengths[n]
+        n += 1
+    if n == 0:
+        n, tot = 1, lengths[0]
+    cu = p.cu_seqlens[: n + 1]
+    sub = PrefillInputs(p.q[:tot], p.k[:tot], p.v[:tot],
+                        None if p.state is None else p.state[:n], p.A_log, p.a[:tot], p.dt_bias,
+                        p.b[:tot], cu, p.scale)
+    t0 = time.perf_counter()
+    prefill_ref(*sub.args())
+    t = time.perf_counter() - t0
+    return {"value": round(tot / t, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle prefill_ref (per-token fp32 loop) on the first {n} sequences "
+                      f"({tot} tokens) of the workload, {t:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all",
+                    help="restrict the run (for profiling)")
+    ap.add_argument("--warm-cache", action="store_true", help="do not rotate buffers")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode and prefill paths shard with no exchange, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from kachua_mlsys_amd import decode, prefill
+    from kachua_mlsys_amd.inputs import decode_config, prefill_config
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    result = {"metric": "decode HBM GB/s + us/step (B=64); prefill tokens/s (varlen 16k tok)",
+              "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+              "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+              "data": "synthetic (seeded randn, BASELINE configs)"}
+
+    # ------------------------------------------------------------ decode ----
+    if args.only in ("all", "decode"):
+        B = 64
+        d0 = decode_config(1)
+        state_b, total_b = decode_bytes(B)
+        nsets = 1 if args.warm_cache else max(2, math.ceil(2 * MALL_BYTES / state_b) + 1)
+        base = d0.to(dev)
+        sets = []
+        for i in range(nsets):
+            st = base.state if i == 0 else base.state.clone()
+            sets.append((st, torch.empty_like(st)))
+        out = torch.empty((B, NV, D), dtype=torch.bfloat16, device=dev)
+
+        def dec_step(s):
+            decode.launch_gdn(base.q, base.k, base.v, s[0], base.A_log, base.a, base.dt_bias,
+                              base.b, base.scale, out, s[1])
+
+        wall_ms, ev_ms, ev_med = time_launches(dec_step, sets, args.steps, args.warmup, torch)
+        us = wall_ms * 1e3
+        result.update({
+            "value": round(state_b / (wall_ms * 1e-3) / 1e9, 1),
+            "ms_per_step": round(wall_ms, 5),
+            "us_per_step": round(us, 3),
+            "config": {"workload": "decode config 1: B=64, one token, fp32 state [64,8,128,128]",
+                       "batch": B, "state_sets_rotated": nsets,
+                       "cache": "warm" if args.warm_cache else "cold (rotation > 256 MiB MALL)"},
+        })
+        traffic = read_traffic("decode_b64_traffic.txt")
+        ach = total_b / (ev_ms * 1e-3) / 1e9
+        result["roofline"] = {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBPS,
+                              "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBPS, 4),
+                              "traffic": traffic, "kernel": "gdn::decode_kernel<32>",
+                              "algorithmic_bytes_per_launch": total_b,
+                              "mean_launch_us": round(ev_ms * 1e3, 3),
+                              "median_launch_us": round(ev_med * 1e3, 3)}
+        # decode B = 1 (configuration 0), launch-latency bound
+        d1 = decode_config(0).to(dev)
+        o1 = torch.empty((1, NV, D), dtype=torch.bfloat16, device=dev)
+        ns1 = torch.empty_like(d1.state)
+        w1, e1, m1 = time_launches(
+            lambda s: decode.launch_gdn(*d1.args(), o1, ns1), [None], max(50, args.steps),
+            args.warmup, torch)
+        result["decode_b1"] = {"us_per_step_wall": round(w1 * 1e3, 3),
+                               "us_per_launch_event_median": round(m1 * 1e3, 3)}
+        del sets
+        torch.cuda.empty_cache()
+
+    # ----------------------------------------------------------- prefill ----
+    if args.only in ("all", "prefill"):
+        pre = {}
+        for cfg in (3, 2, 4):
+            p_cpu = prefill_config(cfg)
+            p = p_cpu.to(dev)
+            T, N = p.q.shape[0], len(p.lengths)
+            ws = torch.empty(prefill.workspace_bytes(N, T), dtype=torch.uint8, device=dev)
+            per_set = prefill_bytes(T, N) + ws.numel()
+            nsets = 1 if args.warm_cache else max(2, math.ceil(2 * MALL_BYTES / per_set) + 1)
+            sets = []
+            for i in range(nsets):
+                q, k, v = (p.q, p.k, p.v) if i == 0 else (p.q.clone(), p.k.clone(), p.v.clone())
+                o = torch.empty((T, NV, D), dtype=torch.bfloat16, device=dev)
+                ns = torch.empty((N, NV, D, D), dtype=torch.float32, device=dev)
+                w = ws if i == 0 else torch.empty_like(ws)
+                sets.append((q, k, v, o, ns, w))
+
+            def pre_step(s):
+                prefill.launch_gdn(s[0], s[1], s[2], p.state, p.A_log, p.a, p.dt_bias, p.b,
+                                   p.cu_seqlens, p.scale, s[3], s[4], workspace=s[5])
+
+            steps = max(10, args.steps // 4)
+            wall_ms, ev_ms, ev_med = time_launches(pre_step, sets, steps, max(3, args.warmup // 4),
+                                                   torch)
+            nbytes = prefill_bytes(T, N)
+            flops = prefill_flops(p.lengths)
+            t_s = ev_ms * 1e-3
+            t_hbm = nbytes / (HBM_PEAK_GBPS * 1e9)
+            t_mfma = flops / (BF16_PEAK_TFLOPS * 1e12)
+            bound = "hbm" if t_hbm >= t_mfma else "mfma"
+            entry = {
+                "tokens": T, "seqs": N, "max_len": max(p.lengths),
+                "us_per_call_wall": round(wall_ms * 1e3, 3),
+                "us_per_call_event_mean": round(ev_ms * 1e3, 3),
+                "us_per_call_event_median": round(ev_med * 1e3, 3),
+                "tokens_per_s": round(T / t_s, 1),
+                "roofline": {"bound": bound,
+                             "achieved": round(nbytes / t_s / 1e9, 1) if bound == "hbm"
+                             else round(flops / t_s / 1e12, 2),
+                             "peak": HBM_PEAK_GBPS if bound == "hbm" else BF16_PEAK_TFLOPS,
+                             "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+                             "frac": round(max(t_hbm, t_mfma) / t_s, 4),
+                             "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
+                             "tflops": round(flops / t_s / 1e12, 2),
+                             "traffic": read_traffic(f"prefill_c{cfg}_traffic.txt")},
+                "cache": "warm" if args.warm_cache else f"cold ({nsets} rotated sets)",
+            }
+            if cfg == 3 and not args.no_cpu:
+                entry["cpu_baseline"] = cpu_prefill_baseline(torch, p_cpu)
+            pre[f"c{cfg}"] = entry
+            del sets, ws
+            torch.cuda.empty_cache()
+        result["prefill"] = pre
+
+    if args.only in ("all", "decode") and not args.no_cpu:
+        result["cpu_baseline"] = cpu_decode_baseline(torch)
+    result["hbm_copy_GBps_measured"] = round(hbm_copy_gbps(torch, dev), 1)
+    result["host"] = {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+                      "device": torch.cuda.get_device_name(dev)}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,104 @@
+"""Build and load ``libgdn_mi355x.so`` (the C ABI declared in include/gdn_mi355x.h).
+
+The library is compiled in-tree with ``hipcc --offload-arch=gfx950`` and loaded
+with ctypes.  Loaded after ``import torch`` it binds to the HIP runtime torch
+already mapped (same soname), so torch's stream handles are valid in it.
+There is no fallback: a missing library raises, it is never replaced by a CPU
+or PyTorch path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import shutil
+import subprocess
+import tempfile
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+CSRC_DIR = PKG_DIR / "csrc"
+INCLUDE_DIR = REPO_DIR / "include"
+LIB_DIR = PKG_DIR / "_lib"
+LIB_PATH = LIB_DIR / "libgdn_mi355x.so"
+SOURCES = ("gdn_decode.hip", "gdn_prefill.hip", "gdn_capi.hip")
+ARCH = "gfx950"
+
+# Every HIP translation unit is built with packed-fp32 instructions disabled.
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-shared", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+# exported symbol -> (restype, argtypes)
+_VP = ctypes.c_void_p
+SIGNATURES = {
+    "gdn_abi_version": (ctypes.c_int, []),
+    "gdn_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "gdn_decode_fwd": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_float,
+                                      _VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
+    "gdn_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_longlong]),
+    "gdn_prefill_fwd": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_longlong, ctypes.c_float, _VP, _VP,
+                                       _VP, ctypes.c_size_t, _VP]),
+}
+ABI_VERSION = 1
+
+
+def hipcc_path() -> str:
+    for cand in (shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the HIP sources into LIB_PATH (atomic replace)."""
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    fd, tmp = tempfile.mkstemp(prefix="libgdn_mi355x.", suffix=".so.tmp", dir=LIB_DIR)
+    os.close(fd)
+    cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", tmp,
+           *[str(CSRC_DIR / s) for s in SOURCES]]
+    try:
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
+        if verbose:
+            print(" ".join(cmd))
+        os.replace(tmp, LIB_PATH)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+    return LIB_PATH
+
+
+_LIB = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the built library (raises if it was never built)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is missing: build it first with "
+            "`python -c 'import __graft_entry__ as g; g.build()'`")
+    import torch  # noqa: F401  (map torch's HIP runtime before ours resolves it)
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    ver = lib.gdn_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
+    _LIB = lib
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().gdn_status_string(status).decode()
+        raise RuntimeError(f"{what} failed with status {status}: {msg}")

@@ -1,0 +1,604 @@
+// GDN prefill: chunked (C = 64) y-space WY recurrence on gfx950 bf16 MFMA.
+//
+// For one v-head and one chunk of c <= 64 tokens with incoming state S ([V, K]),
+// let Gam_t = sum_{i<=t} log g_i (within the chunk), rho[t,i] = exp(Gam_t - Gam_i):
+//   A     = I + strict_lower(beta_t rho[t,i] k_t.k_i),   Tb = A^{-1} diag(beta)
+//   Aqk   = lower(rho[t,i] q_t.k_i)
+//   Delta = Tb (V - diag(gam) K S^T)                     gam_t = exp(Gam_t)
+//   O     = scale (diag(gam) Q S^T + Aqk Delta)
+//   S'    = gam_c S + (diag(tail) Delta)^T K             tail_t = exp(Gam_c - Gam_t)
+// which equals the token recurrence of
+// gdn_prefill_qk4_v8_d128_k_last/solution/reference_torch_impl.py:66-88 exactly
+// in real arithmetic.  All gate factors are bounded ratios (no division by a
+// cumulative decay), so C = 64 is safe where the reference's X-space form
+// (solution/triton/kernel.py:421-425) divides by G.
+//
+// Three launches, all on the caller's stream:
+//   plan     : 1 work-group; chunk records (seq, first token, length) for all
+//              sequences from cu_seqlens, with no host synchronisation.
+//   prepass  : one work-group per (record, v-head), all records in parallel:
+//              gates, K K^T / Q K^T on MFMA, fp32 blocked triangular inverse,
+//              and the packed MFMA operands Tb (bf16 hi+lo), Aqk (bf16),
+//              K^T (bf16) plus gam / tail, written to the workspace.
+//   consumer : one work-group (4 waves) per (seq, v-head, 16-wide V tile),
+//              sequential over the sequence's chunks, state tile in registers.
+//
+// Precision policy (fp32 accumulation everywhere): K, Q, V are bf16 inputs, so
+// their products are exact.  S enters K S^T and Q S^T as a single bf16; Tb and
+// R = V - gam K S^T enter Delta = Tb R as bf16 hi+lo pairs (three MFMAs); the
+// state update uses Delta' = tail Delta as a hi+lo pair; Aqk Delta (output only)
+// is single bf16.  The fp32 state never leaves registers between chunks.
+#include "gdn_common.h"
+#include "../../include/gdn_mi355x.h"
+
+namespace gdn {
+
+constexpr int kChunk = 64;
+constexpr int kBV = 16;                      // consumer V tile
+constexpr int kVTiles = kDim / kBV;          // 8
+constexpr int kFragElems = 4096;             // 64x64 bf16 operand in fragment order
+constexpr int kKTElems = kDim * kChunk;      // 128x64 bf16 K^T in fragment order
+
+// ---- workspace layout -------------------------------------------------------
+struct WsLayout {
+  size_t frag_off;     // bf16 [R][8][3][4096]   (Tb hi, Tb lo, Aqk)
+  size_t gam_off;      // f32  [R][8][2][64]     (gam, tail)
+  size_t kt_off;       // bf16 [R][4][8192]      (K^T)
+  size_t start_off;    // i32  [N + 1]           record start per sequence
+  size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
+  size_t total;
+};
+
+__host__ __device__ inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+__host__ __device__ inline long long max_records(int num_seqs, long long tokens) {
+  return (tokens + kChunk - 1) / kChunk + num_seqs;
+}
+
+__host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
+  WsLayout L;
+  const size_t R = static_cast<size_t>(max_records(num_seqs, tokens));
+  size_t off = 0;
+  L.frag_off = off;  off = align256(off + R * kVHeads * 3 * kFragElems * sizeof(uint16_t));
+  L.gam_off = off;   off = align256(off + R * kVHeads * 2 * kChunk * sizeof(float));
+  L.kt_off = off;    off = align256(off + R * kQKHeads * kKTElems * sizeof(uint16_t));
+  L.start_off = off; off = align256(off + (static_cast<size_t>(num_seqs) + 1) * sizeof(int));
+  L.rec_off = off;   off = align256(off + R * sizeof(int4));
+  L.total = off;
+  return L;
+}
+
+// Sequence bounds from cu_seqlens, clamped into [0, T] with end >= start.
+__device__ __forceinline__ void seq_bounds(const void* cu, int is64, int s, long long T,
+                                           long long& t0, long long& t1) {
+  long long a, b;
+  if (is64) {
+    a = static_cast<const long long*>(cu)[s];
+    b = static_cast<const long long*>(cu)[s + 1];
+  } else {
+    a = static_cast<const int*>(cu)[s];
+    b = static_cast<const int*>(cu)[s + 1];
+  }
+  a = a < 0 ? 0 : (a > T ? T : a);
+  b = b < a ? a : (b > T ? T : b);
+  t0 = a;
+  t1 = b;
+}
+
+// ============================================================================
+// plan: record numbering (exclusive scan of per-sequence chunk counts)
+// ============================================================================
+constexpr int kPlanThreads = 1024;
+
+__global__ __launch_bounds__(kPlanThreads) void plan_kernel(
+    const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
+    int* __restrict__ rec_start, int4* __restrict__ recs) {
+  __shared__ int part[kPlanThreads];
+  const int tid = threadIdx.x;
+  const int per = (num_seqs + kPlanThreads - 1) / kPlanThreads;
+  const int s_begin = tid * per;
+  const int s_end = min(num_seqs, s_begin + per);
+  int local = 0;
+  for (int s = s_begin; s < s_end; ++s) {
+    long long t0, t1;
+    seq_bounds(cu, is64, s, T, t0, t1);
+    local += static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+  }
+  part[tid] = local;
+  __syncthreads();
+  // Hillis-Steele inclusive scan over the per-thread totals
+  for (int off = 1; off < kPlanThreads; off <<= 1) {
+    const int add = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += add;
+    __syncthreads();
+  }
+  int base = part[tid] - local;
+  const int total = min(part[kPlanThreads - 1], R);
+  for (int s = s_begin; s < s_end; ++s) {
+    long long t0, t1;
+    seq_bounds(cu, is64, s, T, t0, t1);
+    rec_start[s] = base;
+    // overlapping (non-monotonic) cu_seqlens can ask for more than R records:
+    // records past the capacity are dropped and the consumer skips them
+    for (long long c0 = t0; c0 < t1; c0 += kChunk, ++base) {
+      const int len = static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0));
+      if (base < R) recs[base] = make_int4(s, static_cast<int>(c0), len, 0);
+    }
+  }
+  if (tid == 0) rec_start[num_seqs] = total;
+  for (int r = total + tid; r < R; r += kPlanThreads) recs[r] = make_int4(-1, 0, 0, 0);
+}
+
+// ============================================================================
+// prepass: chunk-local WY terms for one (record, v-head)
+// ============================================================================
+constexpr int kQKRow = 136;   // bf16 per LDS row of K / Q (128 + 8 pad, 16-byte aligned)
+constexpr int kMRow = 68;     // floats per LDS row of the 64x64 fp32 matrices
+
+struct __align__(16) PrepassSmem {
+  uint16_t kk[kChunk][kQKRow];
+  uint16_t qq[kChunk][kQKRow];
+  float nmat[kChunk][kMRow];      // strict lower beta_t rho K K^T
+  float tmat[kChunk][kMRow];      // first Aqk, then T = (I + N)^{-1}
+  float pscr[4][16][17];          // per-wave 16x16 product scratch
+  float lgam[kChunk];             // Gam_t (log cumulative decay)
+  float beta[kChunk];
+};
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 lds_frag(const uint16_t* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// Lower 16x16 tiles (mi >= ni) of a 4x4 tile grid, in a fixed order.
+__constant__ int kLowerTiles[10][2] = {{0, 0}, {1, 0}, {1, 1}, {2, 0}, {2, 1},
+                                       {2, 2}, {3, 0}, {3, 1}, {3, 2}, {3, 3}};
+
+// P[rows 4(l/16)..+3][col l%16] = sum_u A[r][u] * B[u][c] for 16x16 blocks in LDS.
+__device__ __forceinline__ void block_mma_acc(float (&acc)[4], const float* A, int lda,
+                                              const float* B, int ldb, int r0, int c) {
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const float bv = B[u * ldb + c];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) acc[a] = fmaf(A[(r0 + a) * lda + u], bv, acc[a]);
+  }
+}
+
+__global__ __launch_bounds__(256) void prepass_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
+    const int4* __restrict__ recs, uint16_t* __restrict__ ws_frag,
+    float* __restrict__ ws_gam, uint16_t* __restrict__ ws_kt) {
+  __shared__ PrepassSmem sm;
+  const int r = blockIdx.x;
+  const int h = blockIdx.y;
+  const int hq = h / kGva;
+  const int4 rec = recs[r];
+  const int c = rec.z;
+  if (c <= 0) return;
+  const long long t0 = rec.y;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+
+  // ---- K, Q rows of the chunk into LDS (rows >= c zero) ----
+  for (int idx = tid; idx < kChunk * 16; idx += 256) {
+    const int row = idx >> 4;
+    const int part = idx & 15;
+    uint4 kv = make_uint4(0, 0, 0, 0), qv = make_uint4(0, 0, 0, 0);
+    if (row < c) {
+      const size_t off = ((t0 + row) * kQKHeads + hq) * kDim + part * 8;
+      kv = *reinterpret_cast<const uint4*>(k + off);
+      qv = *reinterpret_cast<const uint4*>(q + off);
+    }
+    *reinterpret_cast<uint4*>(&sm.kk[row][part * 8]) = kv;
+    *reinterpret_cast<uint4*>(&sm.qq[row][part * 8]) = qv;
+  }
+
+  // ---- gates (wave 0): Gam_t inclusive scan of log g, beta ----
+  if (wave == 0) {
+    const int t = lane;
+    float lgv = 0.0f, bet = 0.0f;
+    if (t < c) {
+      const size_t gi = (t0 + t) * kVHeads + h;
+      // clamp: g = e^-100 is already 0 to fp32 working precision, and a finite
+      // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
+      lgv = fmaxf(log_decay(A_log[h], bf2f(a[gi]), dt_bias[h]), -100.0f);
+      bet = sigmoidf(bf2f(b[gi]));
+    }
+    float scan = lgv;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_up(scan, off, 64);
+      if (lane >= off) scan += o;
+    }
+    sm.lgam[t] = scan;
+    sm.beta[t] = bet;
+    const float last = __shfl(scan, c - 1, 64);
+    float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * 2 * kChunk;
+    gp[t] = t < c ? expf(scan) : 0.0f;
+    gp[kChunk + t] = t < c ? expf(last - scan) : 0.0f;
+  }
+  __syncthreads();
+
+  // ---- K K^T and Q K^T lower tiles on MFMA; masked gate weighting ----
+  for (int job = wave; job < 20; job += 4) {
+    const int which = job / 10;                  // 0: K K^T -> N, 1: Q K^T -> Aqk
+    const int mi = kLowerTiles[job % 10][0];
+    const int ni = kLowerTiles[job % 10][1];
+    const uint16_t(*lhs)[kQKRow] = which ? sm.qq : sm.kk;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const bf16x8 av = lds_frag(&lhs[16 * mi + l16][32 * d + 8 * lg]);
+      const bf16x8 bv = lds_frag(&sm.kk[16 * ni + l16][32 * d + 8 * lg]);
+      acc = mfma16(av, bv, acc);
+    }
+    const int col = 16 * ni + l16;
+    const float gcol = sm.lgam[col];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int row = 16 * mi + 4 * lg + rr;
+      const float rho = col <= row ? expf(sm.lgam[row] - gcol) : 0.0f;
+      if (which == 0) {
+        sm.nmat[row][col] = col < row ? sm.beta[row] * rho * acc[rr] : 0.0f;
+      } else {
+        sm.tmat[row][col] = rho * acc[rr];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- pack Aqk (bf16, fragment order; upper triangle zero) ----
+  uint16_t* frag = ws_frag + (static_cast<size_t>(r) * kVHeads + h) * 3 * kFragElems;
+  for (int qi = tid; qi < 512; qi += 256) {
+    const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
+    const int row = 16 * m + (l & 15);
+    const int dep = 32 * d + 8 * (l >> 4);
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i0 = dep + 2 * j, i1 = i0 + 1;
+      const float x0 = i0 <= row ? sm.tmat[row][i0] : 0.0f;
+      const float x1 = i1 <= row ? sm.tmat[row][i1] : 0.0f;
+      w[j] = pack_bf2(x0, x1);
+    }
+    *reinterpret_cast<uint4*>(frag + 2 * kFragElems + qi * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+
+  // ---- K^T in fragment order (once per q/k head, by the even v-head) ----
+  if ((h & 1) == 0) {
+    uint16_t* kt = ws_kt + (static_cast<size_t>(r) * kQKHeads + hq) * kKTElems;
+    for (int qi = tid; qi < 1024; qi += 256) {
+      const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
+      const int kcol = 16 * m + (l & 15);
+      const int t = 32 * d + 8 * (l >> 4);
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        w[j] = static_cast<uint32_t>(sm.kk[t + 2 * j][kcol]) |
+               (static_cast<uint32_t>(sm.kk[t + 2 * j + 1][kcol]) << 16);
+      *reinterpret_cast<uint4*>(kt + qi * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  __syncthreads();   // Aqk consumed from tmat; tmat is free for T
+
+  // ---- T = (I + N)^{-1}: diagonal 16x16 blocks by forward substitution ----
+  if (lane < 16) {
+    const int base = 16 * wave;
+    const int j = lane;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float acc = (i == j) ? 1.0f : 0.0f;
+#pragma unroll
+      for (int m2 = 0; m2 < i; ++m2) acc = fmaf(-sm.nmat[base + i][base + m2], x[m2], acc);
+      x[i] = acc;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sm.tmat[base + i][base + j] = x[i];
+  }
+  __syncthreads();
+
+  // ---- off-diagonal blocks: T_ij = -T_ii sum_{m=j}^{i-1} N_im T_mj, by distance ----
+  const int r0 = 4 * lg;
+  for (int dist = 1; dist < 4; ++dist) {
+    const bool active = wave < 4 - dist;
+    const int bj = wave, bi = wave + dist;
+    if (active) {
+      float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int bm = bj; bm < bi; ++bm)
+        block_mma_acc(p, &sm.nmat[16 * bi][16 * bm], kMRow, &sm.tmat[16 * bm][16 * bj], kMRow,
+                      r0, l16);
+#pragma unroll
+      for (int aa = 0; aa < 4; ++aa) sm.pscr[wave][r0 + aa][l16] = p[aa];
+    }
+    __syncthreads();
+    if (active) {
+      float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      block_mma_acc(t4, &sm.tmat[16 * bi][16 * bi], kMRow, &sm.pscr[wave][0][0], 17, r0, l16);
+#pragma unroll
+      for (int aa = 0; aa < 4; ++aa) sm.tmat[16 * bi + r0 + aa][16 * bj + l16] = -t4[aa];
+    }
+    __syncthreads();
+  }
+
+  // ---- pack Tb = T diag(beta) as bf16 hi + lo (fragment order) ----
+  for (int qi = tid; qi < 512; qi += 256) {
+    const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
+    const int row = 16 * m + (l & 15);
+    const int dep = 32 * d + 8 * (l >> 4);
+    uint32_t wh[4], wl[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i0 = dep + 2 * j, i1 = i0 + 1;
+      const float x0 = i0 <= row ? sm.tmat[row][i0] * sm.beta[i0] : 0.0f;
+      const float x1 = i1 <= row ? sm.tmat[row][i1] * sm.beta[i1] : 0.0f;
+      const uint16_t h0 = f2bf(x0), h1 = f2bf(x1);
+      wh[j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
+      wl[j] = pack_bf2(x0 - bf2f(h0), x1 - bf2f(h1));
+    }
+    *reinterpret_cast<uint4*>(frag + qi * 8) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+    *reinterpret_cast<uint4*>(frag + kFragElems + qi * 8) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+  }
+}
+
+// ============================================================================
+// consumer: sequential chunk loop for one (seq, v-head, 16-wide V tile)
+// ============================================================================
+constexpr int kSRow = 136;    // bf16 per LDS row of S (v-major, k contiguous)
+constexpr int kTRow = 72;     // bf16 per LDS row of the [v][t] operands
+
+struct __align__(16) ConsumerSmem {
+  uint16_t s_bf[kBV][kSRow];      // S tile as bf16, [v][k]
+  uint16_t r_hi[kBV][kTRow];      // R = V - gam K S^T, [v][t]
+  uint16_t r_lo[kBV][kTRow];
+  uint16_t d_o[kBV][kTRow];       // Delta (bf16) for the output
+  uint16_t d_hi[kBV][kTRow];      // tail * Delta, hi / lo, for the state update
+  uint16_t d_lo[kBV][kTRow];
+};
+
+__device__ __forceinline__ bf16x8 gload_frag(const uint16_t* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+
+__device__ __forceinline__ void split_store4(uint16_t* hi_dst, uint16_t* lo_dst, const float (&x)[4]) {
+  uint16_t hv[4];
+  float lv[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hv[i] = f2bf(x[i]);
+    lv[i] = x[i] - bf2f(hv[i]);
+  }
+  *reinterpret_cast<uint2*>(hi_dst) =
+      make_uint2(static_cast<uint32_t>(hv[0]) | (static_cast<uint32_t>(hv[1]) << 16),
+                 static_cast<uint32_t>(hv[2]) | (static_cast<uint32_t>(hv[3]) << 16));
+  *reinterpret_cast<uint2*>(lo_dst) = make_uint2(pack_bf2(lv[0], lv[1]), pack_bf2(lv[2], lv[3]));
+}
+
+__device__ __forceinline__ void store_bf4(uint16_t* dst, const float (&x)[4]) {
+  *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]));
+}
+
+__global__ __launch_bounds__(256) void consumer_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const float* __restrict__ state,
+    const void* __restrict__ cu, int is64, long long T, int R, float scale,
+    const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag,
+    const float* __restrict__ ws_gam, const uint16_t* __restrict__ ws_kt,
+    uint16_t* __restrict__ out, float* __restrict__ new_state) {
+  __shared__ ConsumerSmem sm;
+  const int bid = blockIdx.x;
+  const int s = bid / (kVHeads * kVTiles);
+  const int h = (bid / kVTiles) % kVHeads;
+  const int vt = bid % kVTiles;
+  const int hq = h / kGva;
+  const int v0 = vt * kBV;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6;
+  const int lane = tid & 63;
+  const int l16 = lane & 15;
+  const int lg = lane >> 4;
+
+  long long t0, t1;
+  seq_bounds(cu, is64, s, T, t0, t1);
+
+  // State tile, transposed view S^T[k][v] in MFMA C layout: this wave owns
+  // k = 32w + 16i + 4lg + rr (i < 2, rr < 4) for v = v0 + l16.
+  float* ns_base = new_state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState +
+                   static_cast<size_t>(v0 + l16) * kDim;
+  if (t1 <= t0) {   // empty sequence: the reference leaves new_state zero
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<f32x4*>(ns_base + 32 * w + 16 * i + 4 * lg) = f32x4{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
+  f32x4 st[2];
+  if (state != nullptr) {
+    const float* s_base = state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState +
+                          static_cast<size_t>(v0 + l16) * kDim;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) st[i] = *reinterpret_cast<const f32x4*>(s_base + 32 * w + 16 * i + 4 * lg);
+  } else {
+    st[0] = st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float x[4] = {st[i][0], st[i][1], st[i][2], st[i][3]};
+    store_bf4(&sm.s_bf[l16][32 * w + 16 * i + 4 * lg], x);
+  }
+  __syncthreads();
+
+  int rec = rec_start[s];
+  for (long long c0 = t0; c0 < t1 && rec < R; c0 += kChunk, ++rec) {
+    const int c = static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0));
+    const uint16_t* frag = ws_frag + (static_cast<size_t>(rec) * kVHeads + h) * 3 * kFragElems;
+    const float* gp = ws_gam + (static_cast<size_t>(rec) * kVHeads + h) * 2 * kChunk;
+    const uint16_t* kt = ws_kt + (static_cast<size_t>(rec) * kQKHeads + hq) * kKTElems;
+
+    // ---- stage 1: X = K S^T, Y = Q S^T for token rows 16w .. 16w+15 ----
+    const int arow = 16 * w + l16;
+    f32x4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
+    {
+      const bool ok = arow < c;
+      const size_t off = ((c0 + arow) * kQKHeads + hq) * kDim + 8 * lg;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        bf16x8 ka = {}, qa = {};
+        if (ok) {
+          ka = gload_frag(k + off + 32 * d);
+          qa = gload_frag(q + off + 32 * d);
+        }
+        const bf16x8 sb = lds_frag(&sm.s_bf[l16][32 * d + 8 * lg]);
+        X = mfma16(ka, sb, X);
+        Y = mfma16(qa, sb, Y);
+      }
+    }
+
+    // ---- stage 2: R = V - gam X (hi/lo to LDS), Delta = Tb R ----
+    float gam_r[4], tail_r[4];
+    {
+      float rv[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int t = 16 * w + 4 * lg + rr;
+        gam_r[rr] = gp[t];
+        tail_r[rr] = gp[kChunk + t];
+        const float vv = t < c ? bf2f(v[((c0 + t) * kVHeads + h) * kDim + v0 + l16]) : 0.0f;
+        rv[rr] = vv - gam_r[rr] * X[rr];
+      }
+      split_store4(&sm.r_hi[l16][16 * w + 4 * lg], &sm.r_lo[l16][16 * w + 4 * lg], rv);
+    }
+    __syncthreads();
+    f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int fo = ((w * 2 + d) * 64 + lane) * 8;
+      const bf16x8 th = gload_frag(frag + fo);
+      const bf16x8 tl = gload_frag(frag + kFragElems + fo);
+      const bf16x8 rh = lds_frag(&sm.r_hi[l16][32 * d + 8 * lg]);
+      const bf16x8 rl = lds_frag(&sm.r_lo[l16][32 * d + 8 * lg]);
+      D = mfma16(th, rh, D);
+      D = mfma16(th, rl, D);
+      D = mfma16(tl, rh, D);
+    }
+
+    // ---- stage 3: Delta to LDS; O = scale (gam Y + Aqk Delta) ----
+    {
+      const float dv[4] = {D[0], D[1], D[2], D[3]};
+      float dt[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) dt[rr] = tail_r[rr] * D[rr];
+      store_bf4(&sm.d_o[l16][16 * w + 4 * lg], dv);
+      split_store4(&sm.d_hi[l16][16 * w + 4 * lg], &sm.d_lo[l16][16 * w + 4 * lg], dt);
+    }
+    __syncthreads();
+    {
+      f32x4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int fo = ((w * 2 + d) * 64 + lane) * 8;
+        const bf16x8 aq = gload_frag(frag + 2 * kFragElems + fo);
+        const bf16x8 db = lds_frag(&sm.d_o[l16][32 * d + 8 * lg]);
+        O = mfma16(aq, db, O);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int t = 16 * w + 4 * lg + rr;
+        if (t < c) {
+          const float o = scale * (gam_r[rr] * Y[rr] + O[rr]);
+          out[((c0 + t) * kVHeads + h) * kDim + v0 + l16] = f2bf(o);
+        }
+      }
+    }
+
+    // ---- stage 4: S^T <- gam_c S^T + K^T Delta' for this wave's k rows ----
+    const float gam_c = gp[c - 1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      f32x4 acc = st[i] * gam_c;
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        const int fo = (((2 * w + i) * 2 + d) * 64 + lane) * 8;
+        const bf16x8 ka = gload_frag(kt + fo);
+        const bf16x8 dh = lds_frag(&sm.d_hi[l16][32 * d + 8 * lg]);
+        const bf16x8 dl = lds_frag(&sm.d_lo[l16][32 * d + 8 * lg]);
+        acc = mfma16(ka, dh, acc);
+        acc = mfma16(ka, dl, acc);
+      }
+      st[i] = acc;
+      const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+      store_bf4(&sm.s_bf[l16][32 * w + 16 * i + 4 * lg], x);
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int i = 0; i < 2; ++i) *reinterpret_cast<f32x4*>(ns_base + 32 * w + 16 * i + 4 * lg) = st[i];
+}
+
+}  // namespace gdn
+
+extern "C" size_t gdn_prefill_workspace_bytes(int num_seqs, long long total_tokens) {
+  if (num_seqs < 0 || total_tokens < 0) return 0;
+  return gdn::ws_layout(num_seqs, total_tokens).total;
+}
+
+extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
+                               const float* A_log, const void* a, const float* dt_bias,
+                               const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
+                               int num_seqs, long long total_tokens, float scale, void* output,
+                               float* new_state, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  using namespace gdn;
+  if (num_seqs < 0 || total_tokens < 0) return GDN_ERR_INVALID_ARGUMENT;
+  if (num_seqs == 0) return GDN_OK;
+  if (!cu_seqlens || !new_state || !workspace || !A_log || !dt_bias)
+    return GDN_ERR_INVALID_ARGUMENT;
+  if (total_tokens > 0 && (!q || !k || !v || !a || !b || !output)) return GDN_ERR_INVALID_ARGUMENT;
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15u) return GDN_ERR_UNALIGNED;
+  if ((reinterpret_cast<uintptr_t>(state) | reinterpret_cast<uintptr_t>(new_state)) & 15u)
+    return GDN_ERR_UNALIGNED;
+  if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
+  if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
+  const long long R = max_records(num_seqs, total_tokens);
+  if (R > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * kVTiles > 0x7fffffffLL)
+    return GDN_ERR_INVALID_ARGUMENT;
+  const WsLayout L = ws_layout(num_seqs, total_tokens);
+  if (workspace_bytes < L.total) return GDN_ERR_WORKSPACE_TOO_SMALL;
+  if (!(scale > 0.0f) && !(scale < 0.0f)) scale = 0.08838834764831845f;
+
+  char* ws = static_cast<char*>(workspace);
+  auto* frag = reinterpret_cast<uint16_t*>(ws + L.frag_off);
+  auto* gam = reinterpret_cast<float*>(ws + L.gam_off);
+  auto* kt = reinterpret_cast<uint16_t*>(ws + L.kt_off);
+  auto* rec_start = reinterpret_cast<int*>(ws + L.start_off);
+  auto* recs = reinterpret_cast<int4*>(ws + L.rec_off);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const auto* qb = static_cast<const uint16_t*>(q);
+  const auto* kb = static_cast<const uint16_t*>(k);
+  const auto* vb = static_cast<const uint16_t*>(v);
+  const auto* ab = static_cast<const uint16_t*>(a);
+  const auto* bb = static_cast<const uint16_t*>(b);
+  auto* ob = static_cast<uint16_t*>(output);
+
+  plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
+                                                      total_tokens, static_cast<int>(R), rec_start,
+                                                      recs);
+  prepass_kernel<<<dim3(static_cast<unsigned>(R), kVHeads), dim3(256), 0, st>>>(
+      qb, kb, A_log, ab, dt_bias, bb, recs, frag, gam, kt);
+  consumer_kernel<<<dim3(static_cast<unsigned>(num_seqs * kVHeads * kVTiles)), dim3(256), 0, st>>>(
+      qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, static_cast<int>(R), scale,
+      rec_start, frag, gam,
+      kt, ob, new_state);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? GDN_OK : static_cast<int>(err);
+}

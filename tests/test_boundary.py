@@ -1,0 +1,154 @@
+"""CPU tests of the drop-in boundary: library exports, C-side argument checks,
+Python-side validation and the solution directories.  No kernel is launched:
+the C entry points are only called with arguments they reject before launching.
+"""
+
+import ctypes
+import importlib.util
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from kachua_mlsys_amd import _lib, decode, prefill
+from kachua_mlsys_amd.inputs import decode_inputs, prefill_inputs_from_lengths
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "gdn_mi355x.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        _lib.build()
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = _declared_functions()
+    assert set(names) == set(_lib.SIGNATURES), names
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version_and_status_text(lib):
+    assert lib.gdn_abi_version() == 1
+    assert lib.gdn_status_string(0) == b"ok"
+    for code in (-1, -2, -3, -4):
+        assert b"unknown" not in lib.gdn_status_string(code)
+
+
+def test_workspace_bytes_monotone(lib):
+    w = [lib.gdn_prefill_workspace_bytes(n, t) for n, t in ((1, 64), (1, 65), (2, 65), (16, 16384))]
+    assert all(x % 256 == 0 for x in w)
+    assert w[0] < w[1] < w[2] < w[3]
+    assert lib.gdn_prefill_workspace_bytes(-1, 10) == 0
+
+
+NULL = None
+A16 = 0x10000          # fake, 256-byte aligned addresses: never dereferenced
+A16b = 0x20000
+
+
+def test_c_decode_rejects_before_launch(lib):
+    f = lib.gdn_decode_fwd
+    args = [A16] * 8
+    assert f(*([NULL] + args[1:]), 0.0, A16, A16b, 1, 0, NULL) == -1       # null q
+    assert f(*args, 0.0, A16, A16b, -1, 0, NULL) == -1                     # negative batch
+    assert f(*args, 0.0, A16, A16b, 0, 0, NULL) == 0                       # empty batch: no-op
+    bad = list(args); bad[3] = A16 + 4                                      # state not 16B aligned
+    assert f(*bad, 0.0, A16, A16b, 1, 0, NULL) == -3
+    same = list(args); same[3] = A16b                                       # state == new_state
+    assert f(*same, 0.0, A16, A16b, 1, 0, NULL) == -4
+    assert f(*args, 0.0, A16, A16b, 1, 8, NULL) == -1                      # bad rows_per_wave
+
+
+def test_c_prefill_rejects_before_launch(lib):
+    f = lib.gdn_prefill_fwd
+    ins = [A16] * 8
+    need = lib.gdn_prefill_workspace_bytes(2, 100)
+    base = ins + [A16, 0, 2, 100, 0.0, A16, A16b, A16, need, NULL]
+    x = list(base); x[11] = -1                                              # negative T
+    assert f(*x) == -1
+    x = list(base); x[15] = NULL                                            # no workspace
+    assert f(*x) == -1
+    x = list(base); x[16] = need - 1                                        # workspace too small
+    assert f(*x) == -2
+    x = list(base); x[15] = A16 + 16                                        # workspace not 256B aligned
+    assert f(*x) == -3
+    x = list(base); x[0] = A16 + 8                                          # q not 16B aligned
+    assert f(*x) == -3
+    x = list(base); x[3] = A16b                                             # state aliases new_state
+    assert f(*x) == -4
+    x = list(base); x[10] = 0                                               # no sequences: no-op
+    assert f(*x) == 0
+
+
+# ----------------------------------------------------- Python-side checks ----
+
+def test_decode_validation_errors():
+    d = decode_inputs(2, seed=0)
+    args = list(d.args())
+    bad = list(args); bad[0] = d.q.float()
+    with pytest.raises(TypeError, match="q: expected dtype"):
+        decode.launch_gdn(*bad)
+    bad = list(args); bad[3] = d.state[:, :4]
+    with pytest.raises(ValueError, match="state: expected shape"):
+        decode.launch_gdn(*bad)
+    bad = list(args); bad[1] = d.k.transpose(2, 3).contiguous().transpose(2, 3)
+    with pytest.raises(ValueError, match="k: must be contiguous"):
+        decode.launch_gdn(*bad)
+    with pytest.raises(ValueError, match="alias"):
+        decode.launch_gdn(*args, new_state=d.state)
+    with pytest.raises(ValueError, match="need a GPU"):
+        decode.launch_gdn(*args)          # CPU tensors are well-formed but not on a GPU
+
+
+def test_prefill_validation_errors():
+    p = prefill_inputs_from_lengths([3, 5], seed=0)
+    args = list(p.args())
+    bad = list(args); bad[8] = p.cu_seqlens.float()
+    with pytest.raises(TypeError, match="cu_seqlens"):
+        prefill.launch_gdn(*bad)
+    bad = list(args); bad[6] = p.dt_bias.double()
+    with pytest.raises(TypeError, match="dt_bias"):
+        prefill.launch_gdn(*bad)
+    bad = list(args); bad[2] = p.v[:, :4]
+    with pytest.raises(ValueError, match="v: expected shape"):
+        prefill.launch_gdn(*bad)
+    with pytest.raises(ValueError, match="alias"):
+        prefill.launch_gdn(*args, new_state=p.state)
+    with pytest.raises(ValueError, match="need a GPU"):
+        prefill.launch_gdn(*args)
+    bad = list(args); bad[3] = None                                          # state None is allowed
+    with pytest.raises(ValueError, match="need a GPU"):
+        prefill.launch_gdn(*bad)
+
+
+def test_scale_resolution():
+    from kachua_mlsys_amd._checks import resolve_scale
+    assert resolve_scale(None, 128) == pytest.approx(128 ** -0.5)
+    assert resolve_scale(0.0, 128) == pytest.approx(128 ** -0.5)
+    assert resolve_scale(0.3, 128) == pytest.approx(0.3)
+    assert resolve_scale(torch.tensor(0.5), 128) == pytest.approx(0.5)
+
+
+@pytest.mark.parametrize("definition,module", [("gdn_decode_qk4_v8_d128_k_last", decode),
+                                               ("gdn_prefill_qk4_v8_d128_k_last", prefill)])
+def test_solution_dirs_point_at_entry_points(definition, module):
+    import tomli
+    sol = REPO / "kachua_mlsys_amd" / "solutions" / definition
+    cfg = tomli.loads((sol / "config.toml").read_text())
+    assert cfg["solution"]["definition"] == definition
+    entry_file, fn = cfg["build"]["entry_point"].split("::")
+    spec = importlib.util.spec_from_file_location(f"entry_{definition}", str(sol / entry_file))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert getattr(mod, fn) is module.launch_gdn

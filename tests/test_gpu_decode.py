@@ -1,0 +1,119 @@
+"""GPU parity of the HIP decode kernel (through the C ABI) against the oracle."""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_parity
+from kachua_mlsys_amd import decode
+from kachua_mlsys_amd.inputs import decode_config, decode_inputs
+from oracle.gdn_oracle import decode_ref
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _run(d, dev, **kw):
+    out, ns = decode.launch_gdn(*d.to(dev).args(), **kw)
+    torch.cuda.synchronize()
+    return out, ns
+
+
+@pytest.mark.parametrize("cfg", [0, 1])
+@pytest.mark.parametrize("rows", [0, 16, 32])
+def test_decode_configs(gpu, cfg, rows):
+    d = decode_config(cfg)
+    o_ref, s_ref = decode_ref(*d.args())
+    out, ns = _run(d, gpu, rows_per_wave=rows)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == tuple(o_ref.shape)
+    assert_parity(out, ns, o_ref, s_ref, f"decode c{cfg} rows={rows}")
+
+
+@pytest.mark.parametrize("B", [2, 3, 7, 33])
+def test_decode_batch_sizes(gpu, B):
+    d = decode_inputs(B, seed=100 + B)
+    o_ref, s_ref = decode_ref(*d.args())
+    out, ns = _run(d, gpu)
+    assert_parity(out, ns, o_ref, s_ref, f"decode B={B}")
+
+
+def test_decode_golden_c0(gpu):
+    z = np.load(GOLDEN / "decode_c0.npz")
+
+    def bf(x):
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16).to(gpu)
+
+    def f(x):
+        return torch.from_numpy(np.asarray(x).copy()).to(gpu)
+
+    out, ns = decode.launch_gdn(bf(z["q"]), bf(z["k"]), bf(z["v"]), f(z["state"]), f(z["A_log"]),
+                                bf(z["a"]), f(z["dt_bias"]), bf(z["b"]), float(z["scale"]))
+    torch.cuda.synchronize()
+    assert_parity(out, ns, torch.from_numpy(z["out"]), torch.from_numpy(z["new_state"]),
+                  "decode golden c0")
+
+
+@pytest.mark.parametrize("scale", [None, 0.0, 0.3, -1.5])
+def test_decode_scale(gpu, scale):
+    d = decode_inputs(4, seed=1)
+    d.scale = scale
+    o_ref, s_ref = decode_ref(*d.args())
+    out, ns = _run(d, gpu)
+    assert_parity(out, ns, o_ref, s_ref, f"decode scale={scale}")
+
+
+@pytest.mark.parametrize("case", ["g0", "beta0", "beta1", "big_state"])
+def test_decode_gate_extremes(gpu, case):
+    d = decode_inputs(4, seed=2)
+    if case == "g0":          # g underflows to 0: S' = beta v k^T
+        d.A_log.fill_(3.0)
+        d.a.fill_(30.0)
+    elif case == "beta0":     # beta -> 0: S' = g S
+        d.b.fill_(-30.0)
+    elif case == "beta1":
+        d.b.fill_(30.0)
+    else:
+        d.state.mul_(50.0)
+    o_ref, s_ref = decode_ref(*d.args())
+    out, ns = _run(d, gpu)
+    assert_parity(out, ns, o_ref, s_ref, f"decode {case}")
+
+
+def test_decode_out_4d_and_side_stream(gpu):
+    d = decode_inputs(5, seed=3).to(gpu)
+    out = torch.empty((5, 1, 8, 128), dtype=torch.bfloat16, device=gpu)
+    ns = torch.empty_like(d.state)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        decode.launch_gdn(*d.args(), out, ns)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    o_ref, s_ref = decode_ref(*decode_inputs(5, seed=3).args())
+    assert_parity(out.reshape(5, 8, 128), ns, o_ref, s_ref, "decode 4-D out on a side stream")
+
+
+def test_decode_state_untouched_and_deterministic(gpu):
+    d = decode_inputs(8, seed=4).to(gpu)
+    before = d.state.clone()
+    o1, s1 = decode.launch_gdn(*d.args())
+    o2, s2 = decode.launch_gdn(*d.args())
+    torch.cuda.synchronize()
+    assert torch.equal(d.state, before)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_decode_chain_matches_oracle_chain(gpu):
+    # several steps with new_state fed back as state
+    d = decode_inputs(3, seed=5)
+    st_ref = d.state.clone()
+    st = d.state.to(gpu)
+    for step in range(4):
+        dd = decode_inputs(3, seed=50 + step)
+        o_ref, st_ref = decode_ref(dd.q, dd.k, dd.v, st_ref, d.A_log, dd.a, d.dt_bias, dd.b, None)
+        g = dd.to(gpu)
+        o, st = decode.launch_gdn(g.q, g.k, g.v, st, d.A_log.to(gpu), g.a, d.dt_bias.to(gpu), g.b, None)
+    torch.cuda.synchronize()
+    assert_parity(o, st, o_ref, st_ref, "decode 4-step chain")

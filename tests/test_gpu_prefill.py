@@ -1,0 +1,144 @@
+"""GPU parity of the HIP prefill path (plan + prepass + consumer, through the C ABI).
+
+Full-size configurations 2-4 are checked directly against the fp32 oracle
+(its per-token loop finishes in seconds at these sizes); smaller ragged cases
+cover empty sequences, partial chunks, state=None, int64 cu_seqlens, resume,
+and the prefill -> decode hand-off.
+"""
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import assert_parity, state_rel
+from kachua_mlsys_amd import decode, prefill
+from kachua_mlsys_amd.inputs import prefill_config, prefill_inputs_from_lengths
+from oracle.gdn_oracle import decode_ref, prefill_ref
+
+pytestmark = pytest.mark.gpu
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _check(p, dev, label, **kw):
+    print(f"[case] {label}: lengths={p.lengths[:8]}{'...' if len(p.lengths) > 8 else ''}", flush=True)
+    o_ref, s_ref, o32 = prefill_ref(*p.args(), return_fp32_out=True)
+    out, ns = prefill.launch_gdn(*p.to(dev).args(), **kw)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.bfloat16 and ns.dtype == torch.float32
+    return assert_parity(out, ns, o32, s_ref, label)
+
+
+@pytest.mark.parametrize("cfg", [2, 3, 4])
+def test_prefill_configs(gpu, cfg):
+    _check(prefill_config(cfg), gpu, f"prefill c{cfg}")
+
+
+@pytest.mark.parametrize("lengths", [[1], [63], [64], [65], [0, 1, 63, 64, 65, 0, 130],
+                                     [200, 0, 0, 3], [0]])
+def test_prefill_ragged(gpu, lengths):
+    _check(prefill_inputs_from_lengths(lengths, seed=len(lengths) * 31 + sum(lengths)), gpu,
+           f"prefill ragged {lengths}")
+
+
+def test_prefill_state_none_and_int64(gpu):
+    p = prefill_inputs_from_lengths([90, 17, 64], seed=3, cu_dtype=torch.int64)
+    p.state = None
+    _check(p, gpu, "prefill state=None int64 cu_seqlens")
+
+
+@pytest.mark.parametrize("name", ["prefill_ragged", "prefill_t256_nostate"])
+def test_prefill_golden(gpu, name):
+    z = np.load(GOLDEN / f"{name}.npz")
+
+    def bf(x):
+        return torch.from_numpy(x.view(np.int16).copy()).view(torch.bfloat16).to(gpu)
+
+    def f(x):
+        return torch.from_numpy(np.asarray(x).copy()).to(gpu)
+
+    state = bf(z["state_bf16"]).float() if "state_bf16" in z else None
+    out, ns = prefill.launch_gdn(bf(z["q"]), bf(z["k"]), bf(z["v"]), state, f(z["A_log"]),
+                                 bf(z["a"]), f(z["dt_bias"]), bf(z["b"]), f(z["cu_seqlens"]), None)
+    torch.cuda.synchronize()
+    ref_o = torch.from_numpy(z["out"].view(np.int16).copy()).view(torch.bfloat16).float()
+    assert_parity(out, ns, ref_o, torch.from_numpy(z["new_state"]), f"golden {name}")
+
+
+def test_prefill_strong_decay_and_large_state(gpu):
+    p = prefill_inputs_from_lengths([130, 70], seed=9)
+    p.A_log[:4] = 2.0
+    p.a[:, :4] = 15.0
+    p.state.mul_(40.0)
+    _check(p, gpu, "prefill strong decay / large state")
+
+
+def test_prefill_scale_and_dps_outputs(gpu):
+    p = prefill_inputs_from_lengths([77, 5], seed=10)
+    p.scale = 0.25
+    o_ref, s_ref, o32 = prefill_ref(*p.args(), return_fp32_out=True)
+    g = p.to(gpu)
+    out = torch.full((82, 8, 128), float("nan"), dtype=torch.bfloat16, device=gpu)
+    ns = torch.full((2, 8, 128, 128), float("nan"), device=gpu)
+    r_out, r_ns = prefill.launch_gdn(*g.args(), out, ns)
+    torch.cuda.synchronize()
+    assert r_out.data_ptr() == out.data_ptr() and r_ns.data_ptr() == ns.data_ptr()
+    assert_parity(out, ns, o32, s_ref, "prefill scale=0.25 into caller buffers")
+
+
+def test_prefill_resume_invariant(gpu):
+    p = prefill_inputs_from_lengths([300], seed=11).to(gpu)
+    cut = 129
+    o_all, s_all = prefill.launch_gdn(*p.args())
+    cu_a = torch.tensor([0, cut], dtype=torch.int32, device=gpu)
+    cu_b = torch.tensor([0, 300 - cut], dtype=torch.int32, device=gpu)
+    sl_a, sl_b = slice(0, cut), slice(cut, 300)
+    o_a, s_a = prefill.launch_gdn(p.q[sl_a], p.k[sl_a], p.v[sl_a], p.state, p.A_log, p.a[sl_a],
+                                  p.dt_bias, p.b[sl_a], cu_a, None)
+    o_b, s_b = prefill.launch_gdn(p.q[sl_b], p.k[sl_b], p.v[sl_b], s_a, p.A_log, p.a[sl_b],
+                                  p.dt_bias, p.b[sl_b], cu_b, None)
+    torch.cuda.synchronize()
+    o_split = torch.cat([o_a, o_b]).float()
+    assert torch.allclose(o_split, o_all.float(), atol=1e-2, rtol=1e-2)
+    assert state_rel(s_b, s_all) <= 2e-3
+
+
+def test_prefill_then_decode(gpu):
+    # prefill of T tokens then one decode step == prefill of T + 1 tokens
+    p = prefill_inputs_from_lengths([97], seed=12)
+    T = 96
+    g = p.to(gpu)
+    o_p, s_p = prefill.launch_gdn(g.q[:T], g.k[:T], g.v[:T], g.state, g.A_log, g.a[:T], g.dt_bias,
+                                  g.b[:T], torch.tensor([0, T], dtype=torch.int32, device=gpu), None)
+    o_d, s_d = decode.launch_gdn(g.q[T:].unsqueeze(1), g.k[T:].unsqueeze(1), g.v[T:].unsqueeze(1),
+                                 s_p, g.A_log, g.a[T:].unsqueeze(1), g.dt_bias, g.b[T:].unsqueeze(1),
+                                 None)
+    torch.cuda.synchronize()
+    o_ref, s_ref, o32 = prefill_ref(*p.args(), return_fp32_out=True)
+    assert_parity(o_d, s_d, o32[T:], s_ref, "prefill(96) -> decode(1) vs prefill(97)")
+
+
+def test_prefill_deterministic(gpu):
+    p = prefill_config(2).to(gpu)
+    o1, s1 = prefill.launch_gdn(*p.args())
+    o2, s2 = prefill.launch_gdn(*p.args())
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_prefill_overlapping_cu_seqlens_is_safe(gpu):
+    # malformed (non-monotonic) cu_seqlens: bounds are clamped on the device,
+    # the call completes and the well-formed first sequence is still exact
+    p = prefill_inputs_from_lengths([100], seed=13)
+    cu = torch.tensor([0, 100, 50, 100, 0, 100], dtype=torch.int32)
+    N = 5
+    state = torch.randn(N, 8, 128, 128) * 0.02
+    state[0] = p.state[0]
+    g = p.to(gpu)
+    out, ns = prefill.launch_gdn(g.q, g.k, g.v, state.to(gpu), g.A_log, g.a, g.dt_bias, g.b,
+                                 cu.to(gpu), None)
+    torch.cuda.synchronize()
+    o_ref, s_ref = prefill_ref(*p.args())
+    assert state_rel(ns[0], s_ref[0]) <= 2e-3
+    assert torch.isfinite(ns).all()
