@@ -25,18 +25,17 @@ __device__ __forceinline__ float bf2f(uint16_t x) {
   return __uint_as_float(static_cast<uint32_t>(x) << 16);
 }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+// Round-to-nearest-even fp32 -> bf16.  The __bf16 conversion lowers to
+// gfx950's v_cvt_pk_bf16_f32 (branch-free, NaN stays NaN).
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // Low / high bf16 of a packed pair.
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Two fp32 -> packed bf16 pair (one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
 }
@@ -55,6 +54,12 @@ __device__ __forceinline__ float log_decay(float A_log, float a, float dt_bias) 
 }
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// 2^x on the transcendental unit (v_exp_f32, ~1 ulp).  Used for decay ratios
+// whose exponent is <= 0, where underflow to 0 is the correct limit.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---- cross-lane exchange inside 32-lane halves of a wave64 ------------------
 // XOR partner exchange built from DPP (masks 1, 2, 8) and ds_swizzle bit-mode

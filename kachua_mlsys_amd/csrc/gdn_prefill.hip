@@ -142,7 +142,7 @@ struct __align__(16) PrepassSmem {
   float nmat[kChunk][kMRow];      // strict lower beta_t rho K K^T
   float tmat[kChunk][kMRow];      // first Aqk, then T = (I + N)^{-1}
   float pscr[4][16][17];          // per-wave 16x16 product scratch
-  float lgam[kChunk];             // Gam_t (log cumulative decay)
+  float lgam[kChunk];             // Gam_t / ln 2 (log2 cumulative decay)
   float beta[kChunk];
 };
 
@@ -154,9 +154,12 @@ __device__ __forceinline__ bf16x8 lds_frag(const uint16_t* p) {
   return *reinterpret_cast<const bf16x8*>(p);
 }
 
-// Lower 16x16 tiles (mi >= ni) of a 4x4 tile grid, in a fixed order.
-__constant__ int kLowerTiles[10][2] = {{0, 0}, {1, 0}, {1, 1}, {2, 0}, {2, 1},
-                                       {2, 2}, {3, 0}, {3, 1}, {3, 2}, {3, 3}};
+// j-th lower 16x16 tile (mi >= ni) of a 4x4 tile grid, row by row:
+// (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3).
+__device__ __forceinline__ void lower_tile(int j, int& mi, int& ni) {
+  mi = j >= 6 ? 3 : (j >= 3 ? 2 : (j >= 1 ? 1 : 0));
+  ni = j - mi * (mi + 1) / 2;
+}
 
 // P[rows 4(l/16)..+3][col l%16] = sum_u A[r][u] * B[u][c] for 16x16 blocks in LDS.
 __device__ __forceinline__ void block_mma_acc(float (&acc)[4], const float* A, int lda,
@@ -176,8 +179,9 @@ __global__ __launch_bounds__(256) void prepass_kernel(
     const int4* __restrict__ recs, uint16_t* __restrict__ ws_frag,
     float* __restrict__ ws_gam, uint16_t* __restrict__ ws_kt) {
   __shared__ PrepassSmem sm;
-  const int r = blockIdx.x;
-  const int h = blockIdx.y;
+  // linear id = r * 8 + h: v-head h runs on XCD h, as its consumer does
+  const int r = blockIdx.x / kVHeads;
+  const int h = blockIdx.x % kVHeads;
   const int hq = h / kGva;
   const int4 rec = recs[r];
   const int c = rec.z;
@@ -190,30 +194,38 @@ __global__ __launch_bounds__(256) void prepass_kernel(
   const int lg = lane >> 4;
 
   // ---- K, Q rows of the chunk into LDS (rows >= c zero) ----
-  for (int idx = tid; idx < kChunk * 16; idx += 256) {
-    const int row = idx >> 4;
-    const int part = idx & 15;
-    uint4 kv = make_uint4(0, 0, 0, 0), qv = make_uint4(0, 0, 0, 0);
-    if (row < c) {
-      const size_t off = ((t0 + row) * kQKHeads + hq) * kDim + part * 8;
-      kv = *reinterpret_cast<const uint4*>(k + off);
-      qv = *reinterpret_cast<const uint4*>(q + off);
+  // All loads are issued before any is used (clamped rows, zeroed by select)
+  // so the work-group pays one memory round trip, not one per row group.
+  {
+    uint4 kv[4], qv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + 256 * j;
+      const int row = min(idx >> 4, c - 1);
+      const size_t off = ((t0 + row) * kQKHeads + hq) * kDim + (idx & 15) * 8;
+      kv[j] = *reinterpret_cast<const uint4*>(k + off);
+      qv[j] = *reinterpret_cast<const uint4*>(q + off);
     }
-    *reinterpret_cast<uint4*>(&sm.kk[row][part * 8]) = kv;
-    *reinterpret_cast<uint4*>(&sm.qq[row][part * 8]) = qv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int idx = tid + 256 * j;
+      const int row = idx >> 4;
+      const uint4 z = make_uint4(0, 0, 0, 0);
+      *reinterpret_cast<uint4*>(&sm.kk[row][(idx & 15) * 8]) = row < c ? kv[j] : z;
+      *reinterpret_cast<uint4*>(&sm.qq[row][(idx & 15) * 8]) = row < c ? qv[j] : z;
+    }
   }
 
   // ---- gates (wave 0): Gam_t inclusive scan of log g, beta ----
   if (wave == 0) {
     const int t = lane;
-    float lgv = 0.0f, bet = 0.0f;
-    if (t < c) {
-      const size_t gi = (t0 + t) * kVHeads + h;
-      // clamp: g = e^-100 is already 0 to fp32 working precision, and a finite
-      // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
-      lgv = fmaxf(log_decay(A_log[h], bf2f(a[gi]), dt_bias[h]), -100.0f);
-      bet = sigmoidf(bf2f(b[gi]));
-    }
+    const size_t gi = (t0 + min(t, c - 1)) * kVHeads + h;
+    const float a_t = bf2f(a[gi]), b_t = bf2f(b[gi]);
+    // clamp: g = e^-100 is already 0 to fp32 working precision, and a finite
+    // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
+    // log2 of the decay (Gam kept in log2 units so every ratio is one v_exp_f32)
+    const float lgv = t < c ? fmaxf(log_decay(A_log[h], a_t, dt_bias[h]), -100.0f) * kLog2e : 0.0f;
+    const float bet = t < c ? sigmoidf(b_t) : 0.0f;
     float scan = lgv;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -224,16 +236,16 @@ __global__ __launch_bounds__(256) void prepass_kernel(
     sm.beta[t] = bet;
     const float last = __shfl(scan, c - 1, 64);
     float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * 2 * kChunk;
-    gp[t] = t < c ? expf(scan) : 0.0f;
-    gp[kChunk + t] = t < c ? expf(last - scan) : 0.0f;
+    gp[t] = t < c ? fast_exp2(scan) : 0.0f;
+    gp[kChunk + t] = t < c ? fast_exp2(last - scan) : 0.0f;
   }
   __syncthreads();
 
   // ---- K K^T and Q K^T lower tiles on MFMA; masked gate weighting ----
   for (int job = wave; job < 20; job += 4) {
     const int which = job / 10;                  // 0: K K^T -> N, 1: Q K^T -> Aqk
-    const int mi = kLowerTiles[job % 10][0];
-    const int ni = kLowerTiles[job % 10][1];
+    int mi, ni;
+    lower_tile(job % 10, mi, ni);
     const uint16_t(*lhs)[kQKRow] = which ? sm.qq : sm.kk;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
@@ -247,7 +259,7 @@ __global__ __launch_bounds__(256) void prepass_kernel(
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int row = 16 * mi + 4 * lg + rr;
-      const float rho = col <= row ? expf(sm.lgam[row] - gcol) : 0.0f;
+      const float rho = col <= row ? fast_exp2(sm.lgam[row] - gcol) : 0.0f;
       if (which == 0) {
         sm.nmat[row][col] = col < row ? sm.beta[row] * rho * acc[rr] : 0.0f;
       } else {
@@ -388,6 +400,195 @@ __device__ __forceinline__ void store_bf4(uint16_t* dst, const float (&x)[4]) {
   *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]));
 }
 
+// Per-lane operands of one chunk step, loaded one chunk ahead so that the
+// global-memory latency overlaps the previous chunk's MFMA/LDS chain.
+struct ChunkOps {
+  bf16x8 ka[4], qa[4];       // K, Q rows 16w + l16, k = 32d + 8lg .. +7
+  bf16x8 th[2], tl[2];       // Tb hi / lo fragments (rows 16w.., depth 32d..)
+  bf16x8 aq[2];              // Aqk fragments
+  bf16x8 kt[2][2];           // K^T fragments for k tiles 2w + i
+  f32x4 gam, tail;           // gam_t, tail_t for t = 16w + 4lg + rr
+  uint16_t vv[4];            // V[t][v0 + l16] (bf16)
+  float gam_c;
+  int c;                     // chunk length
+  long long c0;              // first token
+};
+
+// Where a chunk's operands live: first token, length, record index.
+struct ChunkRef {
+  long long c0;
+  int c;
+  int rec;
+};
+
+// Operand loads of one chunk, in three parts issued at different points of the
+// previous steps so that the vector-memory pipe streams them while the MFMA
+// chain runs (issued as one burst they stall the issuing wave for thousands
+// of cycles).  Rows past the chunk end are clamped to the last valid row
+// instead of being masked: unconditional loads keep the prefetch free of wait
+// points, and the duplicate rows are harmless because gam, Tb and the V mask
+// zero R, Delta and every state contribution for t >= c, and their outputs are
+// never stored.
+template <int PART>
+__device__ __forceinline__ void load_chunk_part(
+    ChunkOps& o, const ChunkRef& r, int h, int hq, int v0, int w, int lane,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, const uint16_t* __restrict__ ws_frag,
+    const float* __restrict__ ws_gam, const uint16_t* __restrict__ ws_kt) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  if constexpr (PART == 0) {
+    o.c0 = r.c0;
+    o.c = r.c;
+    const int arow = min(16 * w + l16, r.c - 1);
+    const size_t off = ((r.c0 + arow) * kQKHeads + hq) * kDim + 8 * lg;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      o.ka[d] = gload_frag(k + off + 32 * d);
+      o.qa[d] = gload_frag(q + off + 32 * d);
+    }
+  } else if constexpr (PART == 1) {
+    const uint16_t* frag = ws_frag + (static_cast<size_t>(r.rec) * kVHeads + h) * 3 * kFragElems;
+    const float* gp = ws_gam + (static_cast<size_t>(r.rec) * kVHeads + h) * 2 * kChunk;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int fo = ((w * 2 + d) * 64 + lane) * 8;
+      o.th[d] = gload_frag(frag + fo);
+      o.tl[d] = gload_frag(frag + kFragElems + fo);
+    }
+    const int tb = 16 * w + 4 * lg;
+    o.gam = *reinterpret_cast<const f32x4*>(gp + tb);
+    o.tail = *reinterpret_cast<const f32x4*>(gp + kChunk + tb);
+    o.gam_c = gp[r.c - 1];
+  } else {
+    const uint16_t* frag = ws_frag + (static_cast<size_t>(r.rec) * kVHeads + h) * 3 * kFragElems;
+    const uint16_t* kt = ws_kt + (static_cast<size_t>(r.rec) * kQKHeads + hq) * kKTElems;
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      o.aq[d] = gload_frag(frag + 2 * kFragElems + ((w * 2 + d) * 64 + lane) * 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+        o.kt[i][d] = gload_frag(kt + (((2 * w + i) * 2 + d) * 64 + lane) * 8);
+    const int tb = 16 * w + 4 * lg;
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)     // masked to 0 for t >= c where it is used
+      o.vv[rr] = v[((r.c0 + min(tb + rr, r.c - 1)) * kVHeads + h) * kDim + v0 + l16];
+  }
+}
+
+// Pointers and coordinates every chunk load of one consumer wave shares.
+struct LoadCtx {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* ws_frag;
+  const float* ws_gam;
+  const uint16_t* ws_kt;
+  int h, hq, v0, w, lane;
+};
+
+template <int PART>
+__device__ __forceinline__ void load_part(ChunkOps& o, const ChunkRef& r, const LoadCtx& L) {
+  load_chunk_part<PART>(o, r, L.h, L.hq, L.v0, L.w, L.lane, L.q, L.k, L.v, L.ws_frag, L.ws_gam,
+                        L.ws_kt);
+}
+
+__device__ __forceinline__ void load_chunk_ops(ChunkOps& o, const ChunkRef& r, const LoadCtx& L) {
+  load_part<0>(o, r, L);
+  load_part<1>(o, r, L);
+  load_part<2>(o, r, L);
+}
+
+// One chunk step of the consumer for wave w: reads the state tile from LDS
+// (bf16) and its fp32 C-layout registers st, writes this chunk's outputs and
+// the advanced state.  Three work-group barriers.
+// The operands of chunk `pre` are loaded into `nxt` in three parts between
+// the stages.
+__device__ __forceinline__ void consumer_step(const ChunkOps& cur, ChunkOps& nxt, const ChunkRef& pre,
+                                              const LoadCtx& L, f32x4 (&st)[2], ConsumerSmem& sm,
+                                              int h, int v0, int w, int l16, int lg, float scale,
+                                              uint16_t* __restrict__ out) {
+  const int c = cur.c;
+  const long long c0 = cur.c0;
+  // ---- stage 1: X = K S^T, Y = Q S^T for token rows 16w .. 16w+15 ----
+  f32x4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const bf16x8 sb = lds_frag(&sm.s_bf[l16][32 * d + 8 * lg]);
+    X = mfma16(cur.ka[d], sb, X);
+    Y = mfma16(cur.qa[d], sb, Y);
+  }
+  load_part<0>(nxt, pre, L);
+
+  // ---- stage 2: R = V - gam X (hi/lo to LDS), Delta = Tb R ----
+  {
+    float rv[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const float vv = (16 * w + 4 * lg + rr < c) ? bf2f(cur.vv[rr]) : 0.0f;
+      rv[rr] = vv - cur.gam[rr] * X[rr];
+    }
+    split_store4(&sm.r_hi[l16][16 * w + 4 * lg], &sm.r_lo[l16][16 * w + 4 * lg], rv);
+  }
+  __syncthreads();
+  f32x4 D = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const bf16x8 rh = lds_frag(&sm.r_hi[l16][32 * d + 8 * lg]);
+    const bf16x8 rl = lds_frag(&sm.r_lo[l16][32 * d + 8 * lg]);
+    D = mfma16(cur.th[d], rh, D);
+    D = mfma16(cur.th[d], rl, D);
+    D = mfma16(cur.tl[d], rh, D);
+  }
+  load_part<1>(nxt, pre, L);
+
+  // ---- stage 3: Delta to LDS; O = scale (gam Y + Aqk Delta) ----
+  {
+    const float dv[4] = {D[0], D[1], D[2], D[3]};
+    float dt[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) dt[rr] = cur.tail[rr] * D[rr];
+    store_bf4(&sm.d_o[l16][16 * w + 4 * lg], dv);
+    split_store4(&sm.d_hi[l16][16 * w + 4 * lg], &sm.d_lo[l16][16 * w + 4 * lg], dt);
+  }
+  __syncthreads();
+  {
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const bf16x8 db = lds_frag(&sm.d_o[l16][32 * d + 8 * lg]);
+      O = mfma16(cur.aq[d], db, O);
+    }
+    load_part<2>(nxt, pre, L);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int t = 16 * w + 4 * lg + rr;
+      if (t < c) {
+        const float o = scale * (cur.gam[rr] * Y[rr] + O[rr]);
+        out[((c0 + t) * kVHeads + h) * kDim + v0 + l16] = f2bf(o);
+      }
+    }
+  }
+
+  // ---- stage 4: S^T <- gam_c S^T + K^T Delta' for this wave's k rows ----
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    f32x4 acc = st[i] * cur.gam_c;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const bf16x8 dh = lds_frag(&sm.d_hi[l16][32 * d + 8 * lg]);
+      const bf16x8 dl = lds_frag(&sm.d_lo[l16][32 * d + 8 * lg]);
+      acc = mfma16(cur.kt[i][d], dh, acc);
+      acc = mfma16(cur.kt[i][d], dl, acc);
+    }
+    st[i] = acc;
+    const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
+    store_bf4(&sm.s_bf[l16][32 * w + 16 * i + 4 * lg], x);
+  }
+  __syncthreads();
+}
+
 __global__ __launch_bounds__(256) void consumer_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ state,
@@ -396,10 +597,15 @@ __global__ __launch_bounds__(256) void consumer_kernel(
     const float* __restrict__ ws_gam, const uint16_t* __restrict__ ws_kt,
     uint16_t* __restrict__ out, float* __restrict__ new_state) {
   __shared__ ConsumerSmem sm;
+  // XCD-aware mapping: work-groups are dispatched round-robin over the 8 XCDs
+  // (XCD = linear id % 8).  The 8 V tiles of one (seq, v-head) read identical
+  // chunk operands, so they are given ids that are equal mod 8: they share one
+  // XCD's L2, and v-head h always lands on XCD h (where its prepass ran).
   const int bid = blockIdx.x;
-  const int s = bid / (kVHeads * kVTiles);
-  const int h = (bid / kVTiles) % kVHeads;
-  const int vt = bid % kVTiles;
+  const int grp = (bid / (kVHeads * kVTiles)) * kVHeads + (bid % kVHeads);   // s * 8 + h
+  const int vt = (bid / kVHeads) % kVTiles;
+  const int s = grp / kVHeads;
+  const int h = grp % kVHeads;
   const int hq = h / kGva;
   const int v0 = vt * kBV;
   const int tid = threadIdx.x;
@@ -421,6 +627,25 @@ __global__ __launch_bounds__(256) void consumer_kernel(
       *reinterpret_cast<f32x4*>(ns_base + 32 * w + 16 * i + 4 * lg) = f32x4{0.f, 0.f, 0.f, 0.f};
     return;
   }
+  const int rec0 = rec_start[s];
+  const long long nchunks = (t1 - t0 + kChunk - 1) / kChunk;
+  // chunks whose records exist (overlapping cu_seqlens can exhaust the capacity)
+  const long long nvalid = rec0 >= R ? 0 : min(nchunks, static_cast<long long>(R - rec0));
+
+  const LoadCtx L{q, k, v, ws_frag, ws_gam, ws_kt, h, hq, v0, w, lane};
+  // chunk idx -> operand location; clamped to the last chunk so that the
+  // prefetch beyond the end re-reads valid data instead of being skipped
+  auto chunk_ref = [&](long long idx) {
+    idx = min(idx, nvalid - 1);
+    const long long c0 = t0 + idx * kChunk;
+    return ChunkRef{c0, static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0)),
+                    rec0 + static_cast<int>(idx)};
+  };
+  ChunkOps bufA, bufB, bufC;
+  if (nvalid > 0) {
+    load_chunk_ops(bufA, chunk_ref(0), L);
+    load_chunk_ops(bufB, chunk_ref(1), L);
+  }
   f32x4 st[2];
   if (state != nullptr) {
     const float* s_base = state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState +
@@ -437,108 +662,20 @@ __global__ __launch_bounds__(256) void consumer_kernel(
   }
   __syncthreads();
 
-  int rec = rec_start[s];
-  for (long long c0 = t0; c0 < t1 && rec < R; c0 += kChunk, ++rec) {
-    const int c = static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0));
-    const uint16_t* frag = ws_frag + (static_cast<size_t>(rec) * kVHeads + h) * 3 * kFragElems;
-    const float* gp = ws_gam + (static_cast<size_t>(rec) * kVHeads + h) * 2 * kChunk;
-    const uint16_t* kt = ws_kt + (static_cast<size_t>(rec) * kQKHeads + hq) * kKTElems;
-
-    // ---- stage 1: X = K S^T, Y = Q S^T for token rows 16w .. 16w+15 ----
-    const int arow = 16 * w + l16;
-    f32x4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
-    {
-      const bool ok = arow < c;
-      const size_t off = ((c0 + arow) * kQKHeads + hq) * kDim + 8 * lg;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        bf16x8 ka = {}, qa = {};
-        if (ok) {
-          ka = gload_frag(k + off + 32 * d);
-          qa = gload_frag(q + off + 32 * d);
-        }
-        const bf16x8 sb = lds_frag(&sm.s_bf[l16][32 * d + 8 * lg]);
-        X = mfma16(ka, sb, X);
-        Y = mfma16(qa, sb, Y);
-      }
+  // Three operand buffers in a ring: chunk i + 2 is loading (spread over the
+  // stages of step i) while chunk i computes.  Every consumer_step call site
+  // sees the same loads in flight, so the compiler's wait counts never fall
+  // back to draining everything.
+  if (nvalid > 0) {
+    long long ci = 0;
+    for (;;) {
+      consumer_step(bufA, bufC, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
+      if (++ci >= nvalid) break;
+      consumer_step(bufB, bufA, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
+      if (++ci >= nvalid) break;
+      consumer_step(bufC, bufB, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
+      if (++ci >= nvalid) break;
     }
-
-    // ---- stage 2: R = V - gam X (hi/lo to LDS), Delta = Tb R ----
-    float gam_r[4], tail_r[4];
-    {
-      float rv[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int t = 16 * w + 4 * lg + rr;
-        gam_r[rr] = gp[t];
-        tail_r[rr] = gp[kChunk + t];
-        const float vv = t < c ? bf2f(v[((c0 + t) * kVHeads + h) * kDim + v0 + l16]) : 0.0f;
-        rv[rr] = vv - gam_r[rr] * X[rr];
-      }
-      split_store4(&sm.r_hi[l16][16 * w + 4 * lg], &sm.r_lo[l16][16 * w + 4 * lg], rv);
-    }
-    __syncthreads();
-    f32x4 D = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      const int fo = ((w * 2 + d) * 64 + lane) * 8;
-      const bf16x8 th = gload_frag(frag + fo);
-      const bf16x8 tl = gload_frag(frag + kFragElems + fo);
-      const bf16x8 rh = lds_frag(&sm.r_hi[l16][32 * d + 8 * lg]);
-      const bf16x8 rl = lds_frag(&sm.r_lo[l16][32 * d + 8 * lg]);
-      D = mfma16(th, rh, D);
-      D = mfma16(th, rl, D);
-      D = mfma16(tl, rh, D);
-    }
-
-    // ---- stage 3: Delta to LDS; O = scale (gam Y + Aqk Delta) ----
-    {
-      const float dv[4] = {D[0], D[1], D[2], D[3]};
-      float dt[4];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) dt[rr] = tail_r[rr] * D[rr];
-      store_bf4(&sm.d_o[l16][16 * w + 4 * lg], dv);
-      split_store4(&sm.d_hi[l16][16 * w + 4 * lg], &sm.d_lo[l16][16 * w + 4 * lg], dt);
-    }
-    __syncthreads();
-    {
-      f32x4 O = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        const int fo = ((w * 2 + d) * 64 + lane) * 8;
-        const bf16x8 aq = gload_frag(frag + 2 * kFragElems + fo);
-        const bf16x8 db = lds_frag(&sm.d_o[l16][32 * d + 8 * lg]);
-        O = mfma16(aq, db, O);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int t = 16 * w + 4 * lg + rr;
-        if (t < c) {
-          const float o = scale * (gam_r[rr] * Y[rr] + O[rr]);
-          out[((c0 + t) * kVHeads + h) * kDim + v0 + l16] = f2bf(o);
-        }
-      }
-    }
-
-    // ---- stage 4: S^T <- gam_c S^T + K^T Delta' for this wave's k rows ----
-    const float gam_c = gp[c - 1];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      f32x4 acc = st[i] * gam_c;
-#pragma unroll
-      for (int d = 0; d < 2; ++d) {
-        const int fo = (((2 * w + i) * 2 + d) * 64 + lane) * 8;
-        const bf16x8 ka = gload_frag(kt + fo);
-        const bf16x8 dh = lds_frag(&sm.d_hi[l16][32 * d + 8 * lg]);
-        const bf16x8 dl = lds_frag(&sm.d_lo[l16][32 * d + 8 * lg]);
-        acc = mfma16(ka, dh, acc);
-        acc = mfma16(ka, dl, acc);
-      }
-      st[i] = acc;
-      const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-      store_bf4(&sm.s_bf[l16][32 * w + 16 * i + 4 * lg], x);
-    }
-    __syncthreads();
   }
 
 #pragma unroll
@@ -570,7 +707,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
   if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
   const long long R = max_records(num_seqs, total_tokens);
-  if (R > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * kVTiles > 0x7fffffffLL)
+  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * kVTiles > 0x7fffffffLL)
     return GDN_ERR_INVALID_ARGUMENT;
   const WsLayout L = ws_layout(num_seqs, total_tokens);
   if (workspace_bytes < L.total) return GDN_ERR_WORKSPACE_TOO_SMALL;
@@ -593,7 +730,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                       total_tokens, static_cast<int>(R), rec_start,
                                                       recs);
-  prepass_kernel<<<dim3(static_cast<unsigned>(R), kVHeads), dim3(256), 0, st>>>(
+  prepass_kernel<<<dim3(static_cast<unsigned>(R * kVHeads)), dim3(256), 0, st>>>(
       qb, kb, A_log, ab, dt_bias, bb, recs, frag, gam, kt);
   consumer_kernel<<<dim3(static_cast<unsigned>(num_seqs * kVHeads * kVTiles)), dim3(256), 0, st>>>(
       qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, static_cast<int>(R), scale,
