@@ -18,6 +18,10 @@ constexpr int kHeadState = kDim * kDim;     // floats per (seq, v-head) state ti
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
+// Native vectors for raw 16- / 8-byte payloads (HIP's uint4 / uint2 are union
+// structs that scalar replacement cannot split, which forces them to memory).
+typedef __attribute__((ext_vector_type(4))) unsigned u32x4;
+typedef __attribute__((ext_vector_type(2))) unsigned u32x2;
 
 // ---- bf16 <-> fp32 (bit-level; bf16 is carried as uint16_t) ----------------
 

@@ -370,6 +370,11 @@ constexpr int kSRow = 136;    // bf16 per LDS row of S (v-major, k contiguous)
 constexpr int kTRow = 72;     // bf16 per LDS row of the [v][t] operands
 
 struct __align__(16) ConsumerSmem {
+  // Wave-private staging of the chunk's K / Q rows (16 rows per wave, 16-byte
+  // k-chunks XOR-swizzled by row so fragment reads and row writes are both
+  // bank-conflict free) and of its V rows (16 rows x 16 values).
+  uint16_t kq[4][2][16][kDim];
+  uint16_t vs[4][16][kBV];
   uint16_t s_bf[kBV][kSRow];      // S tile as bf16, [v][k]
   uint16_t r_hi[kBV][kTRow];      // R = V - gam K S^T, [v][t]
   uint16_t r_lo[kBV][kTRow];
@@ -403,12 +408,12 @@ __device__ __forceinline__ void store_bf4(uint16_t* dst, const float (&x)[4]) {
 // Per-lane operands of one chunk step, loaded one chunk ahead so that the
 // global-memory latency overlaps the previous chunk's MFMA/LDS chain.
 struct ChunkOps {
-  bf16x8 ka[4], qa[4];       // K, Q rows 16w + l16, k = 32d + 8lg .. +7
+  u32x4 kr[4], qr[4];        // K, Q rows 16w + 4i + lane/16, 16-byte k-chunk lane%16
   bf16x8 th[2], tl[2];       // Tb hi / lo fragments (rows 16w.., depth 32d..)
   bf16x8 aq[2];              // Aqk fragments
   bf16x8 kt[2][2];           // K^T fragments for k tiles 2w + i
   f32x4 gam, tail;           // gam_t, tail_t for t = 16w + 4lg + rr
-  uint16_t vv[4];            // V[t][v0 + l16] (bf16)
+  u32x2 vr;                  // V row 16w + lane/4, values v0 + 4(lane%4) .. +3
   float gam_c;
   int c;                     // chunk length
   long long c0;              // first token
@@ -437,14 +442,20 @@ __device__ __forceinline__ void load_chunk_part(
     const float* __restrict__ ws_gam, const uint16_t* __restrict__ ws_kt) {
   const int l16 = lane & 15, lg = lane >> 4;
   if constexpr (PART == 0) {
+    // 16 lanes read one 256-byte head row, so each load covers 4 whole rows
     o.c0 = r.c0;
     o.c = r.c;
-    const int arow = min(16 * w + l16, r.c - 1);
-    const size_t off = ((r.c0 + arow) * kQKHeads + hq) * kDim + 8 * lg;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      o.ka[d] = gload_frag(k + off + 32 * d);
-      o.qa[d] = gload_frag(q + off + 32 * d);
+    for (int i = 0; i < 4; ++i) {
+      const int row = min(16 * w + 4 * i + lg, r.c - 1);
+      const size_t off = ((r.c0 + row) * kQKHeads + hq) * kDim + 8 * l16;
+      o.kr[i] = *reinterpret_cast<const u32x4*>(k + off);
+      o.qr[i] = *reinterpret_cast<const u32x4*>(q + off);
+    }
+    {
+      const int row = min(16 * w + (lane >> 2), r.c - 1);   // masked to 0 for t >= c where used
+      o.vr = *reinterpret_cast<const u32x2*>(v + ((r.c0 + row) * kVHeads + h) * kDim + v0 +
+                                             4 * (lane & 3));
     }
   } else if constexpr (PART == 1) {
     const uint16_t* frag = ws_frag + (static_cast<size_t>(r.rec) * kVHeads + h) * 3 * kFragElems;
@@ -470,11 +481,25 @@ __device__ __forceinline__ void load_chunk_part(
 #pragma unroll
       for (int d = 0; d < 2; ++d)
         o.kt[i][d] = gload_frag(kt + (((2 * w + i) * 2 + d) * 64 + lane) * 8);
-    const int tb = 16 * w + 4 * lg;
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr)     // masked to 0 for t >= c where it is used
-      o.vv[rr] = v[((r.c0 + min(tb + rr, r.c - 1)) * kVHeads + h) * kDim + v0 + l16];
   }
+}
+
+// Raw K / Q / V rows of a chunk -> this wave's LDS staging area.
+__device__ __forceinline__ void stage_rows(const ChunkOps& o, ConsumerSmem& sm, int w, int lane) {
+  const int l16 = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * i + lg;
+    *reinterpret_cast<u32x4*>(&sm.kq[w][0][row][8 * (l16 ^ row)]) = o.kr[i];
+    *reinterpret_cast<u32x4*>(&sm.kq[w][1][row][8 * (l16 ^ row)]) = o.qr[i];
+  }
+  *reinterpret_cast<u32x2*>(&sm.vs[w][lane >> 2][4 * (lane & 3)]) = o.vr;
+}
+
+// A fragment d (k = 32d + 8lg .. +7 of row l16) of the staged K (m = 0) or Q (m = 1).
+__device__ __forceinline__ bf16x8 staged_frag(const ConsumerSmem& sm, int w, int m, int d,
+                                              int l16, int lg) {
+  return *reinterpret_cast<const bf16x8*>(&sm.kq[w][m][l16][8 * ((4 * d + lg) ^ l16)]);
 }
 
 // Pointers and coordinates every chunk load of one consumer wave shares.
@@ -504,8 +529,10 @@ __device__ __forceinline__ void load_chunk_ops(ChunkOps& o, const ChunkRef& r, c
 // (bf16) and its fp32 C-layout registers st, writes this chunk's outputs and
 // the advanced state.  Three work-group barriers.
 // The operands of chunk `pre` are loaded into `nxt` in three parts between
-// the stages.
-__device__ __forceinline__ void consumer_step(const ChunkOps& cur, ChunkOps& nxt, const ChunkRef& pre,
+// the stages; the raw rows of the following chunk (`mid`) replace this
+// chunk's in the wave's staging area once its fragments are in registers.
+__device__ __forceinline__ void consumer_step(const ChunkOps& cur, const ChunkOps& mid, ChunkOps& nxt,
+                                              const ChunkRef& pre,
                                               const LoadCtx& L, f32x4 (&st)[2], ConsumerSmem& sm,
                                               int h, int v0, int w, int l16, int lg, float scale,
                                               uint16_t* __restrict__ out) {
@@ -513,12 +540,22 @@ __device__ __forceinline__ void consumer_step(const ChunkOps& cur, ChunkOps& nxt
   const long long c0 = cur.c0;
   // ---- stage 1: X = K S^T, Y = Q S^T for token rows 16w .. 16w+15 ----
   f32x4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
+  bf16x8 ka[4], qa[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    ka[d] = staged_frag(sm, w, 0, d, l16, lg);
+    qa[d] = staged_frag(sm, w, 1, d, l16, lg);
+  }
+  uint16_t vv[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) vv[rr] = sm.vs[w][4 * lg + rr][l16];
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     const bf16x8 sb = lds_frag(&sm.s_bf[l16][32 * d + 8 * lg]);
-    X = mfma16(cur.ka[d], sb, X);
-    Y = mfma16(cur.qa[d], sb, Y);
+    X = mfma16(ka[d], sb, X);
+    Y = mfma16(qa[d], sb, Y);
   }
+  stage_rows(mid, sm, w, L.lane);
   load_part<0>(nxt, pre, L);
 
   // ---- stage 2: R = V - gam X (hi/lo to LDS), Delta = Tb R ----
@@ -526,8 +563,8 @@ __device__ __forceinline__ void consumer_step(const ChunkOps& cur, ChunkOps& nxt
     float rv[4];
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
-      const float vv = (16 * w + 4 * lg + rr < c) ? bf2f(cur.vv[rr]) : 0.0f;
-      rv[rr] = vv - cur.gam[rr] * X[rr];
+      const float vf = (16 * w + 4 * lg + rr < c) ? bf2f(vv[rr]) : 0.0f;
+      rv[rr] = vf - cur.gam[rr] * X[rr];
     }
     split_store4(&sm.r_hi[l16][16 * w + 4 * lg], &sm.r_lo[l16][16 * w + 4 * lg], rv);
   }
@@ -589,7 +626,9 @@ __device__ __forceinline__ void consumer_step(const ChunkOps& cur, ChunkOps& nxt
   __syncthreads();
 }
 
-__global__ __launch_bounds__(256) void consumer_kernel(
+// One work-group per CU by design (4 waves, one per SIMD): the register ring
+// of chunk operands needs the whole 512-entry VGPR+AGPR file of a SIMD.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void consumer_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const float* __restrict__ state,
     const void* __restrict__ cu, int is64, long long T, int R, float scale,
@@ -645,6 +684,7 @@ __global__ __launch_bounds__(256) void consumer_kernel(
   if (nvalid > 0) {
     load_chunk_ops(bufA, chunk_ref(0), L);
     load_chunk_ops(bufB, chunk_ref(1), L);
+    stage_rows(bufA, sm, w, lane);
   }
   f32x4 st[2];
   if (state != nullptr) {
@@ -669,11 +709,11 @@ __global__ __launch_bounds__(256) void consumer_kernel(
   if (nvalid > 0) {
     long long ci = 0;
     for (;;) {
-      consumer_step(bufA, bufC, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
+      consumer_step(bufA, bufB, bufC, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
       if (++ci >= nvalid) break;
-      consumer_step(bufB, bufA, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
+      consumer_step(bufB, bufC, bufA, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
       if (++ci >= nvalid) break;
-      consumer_step(bufC, bufB, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
+      consumer_step(bufC, bufA, bufB, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
       if (++ci >= nvalid) break;
     }
   }
