@@ -18,10 +18,14 @@
 //              sequences from cu_seqlens, with no host synchronisation.
 //   prepass  : one work-group per (record, v-head), all records in parallel:
 //              gates, K K^T / Q K^T on MFMA, fp32 blocked triangular inverse,
-//              and the packed MFMA operands Tb (bf16 hi+lo), Aqk (bf16),
-//              K^T (bf16) plus gam / tail, written to the workspace.
-//   consumer : one work-group (4 waves) per (seq, v-head, 16-wide V tile),
-//              sequential over the sequence's chunks, state tile in registers.
+//              and the packed MFMA operands Tb (bf16 hi+lo), Aqk (bf16) plus
+//              gam / tail, written to the workspace.
+//   consumer : one work-group per (seq, v-head); each of its 8 waves (two per
+//              SIMD) owns one 16-wide V tile and runs the whole chunk
+//              recurrence for it with the state in MFMA registers; the chunk
+//              operands (K, Q, V rows, packed Tb / Aqk, gates) are copied from
+//              global memory straight into double-buffered LDS and shared by
+//              the 8 waves.
 //
 // Precision policy (fp32 accumulation everywhere): K, Q, V are bf16 inputs, so
 // their products are exact.  S enters K S^T and Q S^T as a single bf16; Tb and
@@ -34,16 +38,27 @@
 namespace gdn {
 
 constexpr int kChunk = 64;
-constexpr int kBV = 16;                      // consumer V tile
-constexpr int kVTiles = kDim / kBV;          // 8
 constexpr int kFragElems = 4096;             // 64x64 bf16 operand in fragment order
-constexpr int kKTElems = kDim * kChunk;      // 128x64 bf16 K^T in fragment order
+
+// MFMA operands in "permuted fragment order".  For v_mfma_f32_16x16x32_bf16
+// the hardware pairs slot s of lane group lg in A with the same slot of the
+// same lane group in B, so the depth index behind each (lg, s) is ours to
+// choose as long as A and B agree.  This build uses
+//     depth(d, lg, s) = 32 d + 16 (s >> 2) + 4 lg + (s & 3)
+// which is exactly the row index a 16x16 MFMA result (C layout: lane (lg, l16)
+// holds rows 4 lg + rr of tiles 2d and 2d+1) already holds in its registers.
+// Results of one MFMA can therefore be fed back as the B operand of the next
+// with no cross-lane movement.  A 64x64 matrix M is stored as fragments
+// (m = row tile, d = depth chunk): element ((m*2 + d)*64 + lane)*8 + s is
+// M[16m + lane%16][depth(d, lane/16, s)].
+__host__ __device__ constexpr int perm_depth(int d, int lg, int s) {
+  return 32 * d + 16 * (s >> 2) + 4 * lg + (s & 3);
+}
 
 // ---- workspace layout -------------------------------------------------------
 struct WsLayout {
   size_t frag_off;     // bf16 [R][8][3][4096]   (Tb hi, Tb lo, Aqk)
   size_t gam_off;      // f32  [R][8][2][64]     (gam, tail)
-  size_t kt_off;       // bf16 [R][4][8192]      (K^T)
   size_t start_off;    // i32  [N + 1]           record start per sequence
   size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
   size_t total;
@@ -61,7 +76,6 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   size_t off = 0;
   L.frag_off = off;  off = align256(off + R * kVHeads * 3 * kFragElems * sizeof(uint16_t));
   L.gam_off = off;   off = align256(off + R * kVHeads * 2 * kChunk * sizeof(float));
-  L.kt_off = off;    off = align256(off + R * kQKHeads * kKTElems * sizeof(uint16_t));
   L.start_off = off; off = align256(off + (static_cast<size_t>(num_seqs) + 1) * sizeof(int));
   L.rec_off = off;   off = align256(off + R * sizeof(int4));
   L.total = off;
@@ -131,28 +145,45 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 }
 
 // ============================================================================
-// prepass: chunk-local WY terms for one (record, v-head)
+// device helpers shared by the prepass and the consumer
 // ============================================================================
-constexpr int kQKRow = 136;   // bf16 per LDS row of K / Q (128 + 8 pad, 16-byte aligned)
-constexpr int kMRow = 68;     // floats per LDS row of the 64x64 fp32 matrices
-
-struct __align__(16) PrepassSmem {
-  uint16_t kk[kChunk][kQKRow];
-  uint16_t qq[kChunk][kQKRow];
-  float nmat[kChunk][kMRow];      // strict lower beta_t rho K K^T
-  float tmat[kChunk][kMRow];      // first Aqk, then T = (I + N)^{-1}
-  float pscr[4][16][17];          // per-wave 16x16 product scratch
-  float lgam[kChunk];             // Gam_t / ln 2 (log2 cumulative decay)
-  float beta[kChunk];
-};
-
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ bf16x8 lds_frag(const uint16_t* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
+__device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
+
+// K / Q rows in LDS keep natural column order; the 16-byte chunk j of row t is
+// stored at position j ^ kq_swz(t).  kq_swz is a bijection of t & 15, so the
+// row reads (8 consecutive k of 16 rows) and the transposed reads (4
+// consecutive k of 4 rows x 4 chunks) are bank-conflict free.
+__device__ __forceinline__ int kq_swz(int t) { return ((t & 3) << 2) | ((t >> 2) & 3); }
+
+// 16 bytes per lane from global memory straight into LDS: lane i of the wave
+// writes bytes [16 i, 16 i + 16) after the wave-uniform LDS address.
+__device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
+}
+
+// ============================================================================
+// prepass: chunk-local WY terms for one (record, v-head)
+// ============================================================================
+constexpr int kPrepassThreads = 256;
+constexpr int kMRow = 68;     // floats per LDS row of the 64x64 fp32 matrices (16-byte aligned)
+
+// 50 KB: three work-groups per CU.  T reuses the K / Q rows' space once the
+// grams have been formed.
+struct __align__(16) PrepassSmem {
+  union {
+    uint16_t kq[2][kChunk][kDim];   // K, Q rows (bf16, chunk-swizzled)
+    float tm[kChunk][kMRow];        // T = (I + N)^{-1}
+  } u;
+  float nm[kChunk][kMRow];          // N = strict lower beta_t rho K K^T; upper blocks are scratch
+  float lgam[kChunk];               // Gam_t / ln 2 (log2 cumulative decay)
+  float beta[kChunk];
+};
 
 // j-th lower 16x16 tile (mi >= ni) of a 4x4 tile grid, row by row:
 // (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3).
@@ -161,23 +192,26 @@ __device__ __forceinline__ void lower_tile(int j, int& mi, int& ni) {
   ni = j - mi * (mi + 1) / 2;
 }
 
-// P[rows 4(l/16)..+3][col l%16] = sum_u A[r][u] * B[u][c] for 16x16 blocks in LDS.
-__device__ __forceinline__ void block_mma_acc(float (&acc)[4], const float* A, int lda,
-                                              const float* B, int ldb, int r0, int c) {
+// acc += X Y for 16x16 fp32 blocks in LDS (row stride kMRow) on fp32 MFMA;
+// result in C layout (lane (lg, l16) holds rows 4 lg .. 4 lg + 3 of column l16).
+__device__ __forceinline__ f32x4 block_prod(f32x4 acc, const float* X, const float* Y, int l16, int lg) {
 #pragma unroll
-  for (int u = 0; u < 16; ++u) {
-    const float bv = B[u * ldb + c];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) acc[a] = fmaf(A[(r0 + a) * lda + u], bv, acc[a]);
-  }
+  for (int kc = 0; kc < 4; ++kc)
+    acc = mfma_f32(X[l16 * kMRow + 4 * kc + lg], Y[(4 * kc + lg) * kMRow + l16], acc);
+  return acc;
 }
 
-__global__ __launch_bounds__(256) void prepass_kernel(
+__device__ __forceinline__ void block_store(float* Z, const f32x4& v, float sc, int l16, int lg) {
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) Z[(4 * lg + rr) * kMRow + l16] = sc * v[rr];
+}
+
+__global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const int4* __restrict__ recs, uint16_t* __restrict__ ws_frag,
-    float* __restrict__ ws_gam, uint16_t* __restrict__ ws_kt) {
+    float* __restrict__ ws_gam) {
   __shared__ PrepassSmem sm;
   // linear id = r * 8 + h: v-head h runs on XCD h, as its consumer does
   const int r = blockIdx.x / kVHeads;
@@ -188,43 +222,44 @@ __global__ __launch_bounds__(256) void prepass_kernel(
   if (c <= 0) return;
   const long long t0 = rec.y;
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
 
-  // ---- K, Q rows of the chunk into LDS (rows >= c zero) ----
-  // All loads are issued before any is used (clamped rows, zeroed by select)
-  // so the work-group pays one memory round trip, not one per row group.
+  // gate inputs first (wave 0, lane = token): their latency overlaps the row copies
+  float a_t = 0.0f, b_t = 0.0f, alog = 0.0f, dtb = 0.0f;
+  if (w == 0) {
+    const size_t gi = (t0 + min(lane, c - 1)) * kVHeads + h;
+    a_t = bf2f(a[gi]);
+    b_t = bf2f(b[gi]);
+    alog = A_log[h];
+    dtb = dt_bias[h];
+  }
+
+  // ---- K, Q rows of the chunk, copied straight into LDS ----
+  // Rows past the chunk end repeat row c-1: they meet beta = 0 (rows of N),
+  // i <= t masks (columns) and rows of Aqk whose outputs are never stored.
   {
-    uint4 kv[4], qv[4];
+    const size_t qk0 = (static_cast<size_t>(t0) * kQKHeads + hq) * kDim;
+    const char* kb = reinterpret_cast<const char*>(k + qk0);
+    const char* qb = reinterpret_cast<const char*>(q + qk0);
+    const int row0 = 4 * w + (lane >> 4);          // + 16 j keeps row & 15
+    const uint32_t col = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(row0));
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 256 * j;
-      const int row = min(idx >> 4, c - 1);
-      const size_t off = ((t0 + row) * kQKHeads + hq) * kDim + (idx & 15) * 8;
-      kv[j] = *reinterpret_cast<const uint4*>(k + off);
-      qv[j] = *reinterpret_cast<const uint4*>(q + off);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 256 * j;
-      const int row = idx >> 4;
-      const uint4 z = make_uint4(0, 0, 0, 0);
-      *reinterpret_cast<uint4*>(&sm.kk[row][(idx & 15) * 8]) = row < c ? kv[j] : z;
-      *reinterpret_cast<uint4*>(&sm.qq[row][(idx & 15) * 8]) = row < c ? qv[j] : z;
+      const uint32_t off = static_cast<uint32_t>(min(row0 + 16 * j, c - 1)) * (kQKHeads * kDim * 2) + col;
+      dma16(kb + off, &sm.u.kq[0][16 * j + 4 * w][0]);
+      dma16(qb + off, &sm.u.kq[1][16 * j + 4 * w][0]);
     }
   }
 
-  // ---- gates (wave 0): Gam_t inclusive scan of log g, beta ----
-  if (wave == 0) {
+  // ---- gates (wave 0, lane = token): Gam_t inclusive scan of log2 g, beta ----
+  if (w == 0) {
     const int t = lane;
-    const size_t gi = (t0 + min(t, c - 1)) * kVHeads + h;
-    const float a_t = bf2f(a[gi]), b_t = bf2f(b[gi]);
     // clamp: g = e^-100 is already 0 to fp32 working precision, and a finite
     // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
-    // log2 of the decay (Gam kept in log2 units so every ratio is one v_exp_f32)
-    const float lgv = t < c ? fmaxf(log_decay(A_log[h], a_t, dt_bias[h]), -100.0f) * kLog2e : 0.0f;
+    const float lgv = t < c ? fmaxf(log_decay(alog, a_t, dtb), -100.0f) * kLog2e : 0.0f;
     const float bet = t < c ? sigmoidf(b_t) : 0.0f;
     float scan = lgv;
 #pragma unroll
@@ -241,183 +276,203 @@ __global__ __launch_bounds__(256) void prepass_kernel(
   }
   __syncthreads();
 
-  // ---- K K^T and Q K^T lower tiles on MFMA; masked gate weighting ----
-  for (int job = wave; job < 20; job += 4) {
-    const int which = job / 10;                  // 0: K K^T -> N, 1: Q K^T -> Aqk
+  // ---- grams on MFMA: N (K K^T, to LDS) and Aqk (Q K^T, to the workspace) ----
+  // Q K^T is formed transposed (A = K rows, B = Q rows): lane (lg, l16) then
+  // holds Aqk[16 mi + l16][16 ni + 4 lg + rr], which is exactly half (slots
+  // 4 (ni & 1) .. +3) of fragment (mi, ni >> 1) in permuted fragment order.
+  uint16_t* frag = ws_frag + (static_cast<size_t>(r) * kVHeads + h) * 3 * kFragElems;
+  const int rsw = kq_swz(l16);
+  // wave w forms lower tiles j = w, w + 4, w + 8 (< 10) of both grams; all
+  // twelve accumulator chains are independent, so their MFMAs interleave
+  f32x4 akk[3], aqk[3];
+#pragma unroll
+  for (int n = 0; n < 3; ++n) {
     int mi, ni;
-    lower_tile(job % 10, mi, ni);
-    const uint16_t(*lhs)[kQKRow] = which ? sm.qq : sm.kk;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    lower_tile(min(w + 4 * n, 9), mi, ni);
+    akk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    aqk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const bf16x8 av = lds_frag(&lhs[16 * mi + l16][32 * d + 8 * lg]);
-      const bf16x8 bv = lds_frag(&sm.kk[16 * ni + l16][32 * d + 8 * lg]);
-      acc = mfma16(av, bv, acc);
+      const int at = 8 * ((4 * d + lg) ^ rsw);
+      const bf16x8 km = *reinterpret_cast<const bf16x8*>(&sm.u.kq[0][16 * mi + l16][at]);
+      const bf16x8 kn = *reinterpret_cast<const bf16x8*>(&sm.u.kq[0][16 * ni + l16][at]);
+      const bf16x8 qm = *reinterpret_cast<const bf16x8*>(&sm.u.kq[1][16 * mi + l16][at]);
+      akk[n] = mfma16(km, kn, akk[n]);
+      aqk[n] = mfma16(kn, qm, aqk[n]);
     }
-    const int col = 16 * ni + l16;
-    const float gcol = sm.lgam[col];
+  }
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int row = 16 * mi + 4 * lg + rr;
-      const float rho = col <= row ? fast_exp2(sm.lgam[row] - gcol) : 0.0f;
-      if (which == 0) {
-        sm.nmat[row][col] = col < row ? sm.beta[row] * rho * acc[rr] : 0.0f;
-      } else {
-        sm.tmat[row][col] = rho * acc[rr];
+  for (int n = 0; n < 3; ++n) {
+    if (w + 4 * n >= 10) break;   // wave-uniform
+    int mi, ni;
+    lower_tile(w + 4 * n, mi, ni);
+    {
+      // akk[n][rr] = K_t . K_i, t = 16 mi + 4 lg + rr, i = 16 ni + l16
+      const int i = 16 * ni + l16;
+      const float gi_ = sm.lgam[i];
+      const f32x4 gt = *reinterpret_cast<const f32x4*>(&sm.lgam[16 * mi + 4 * lg]);
+      const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[16 * mi + 4 * lg]);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int t = 16 * mi + 4 * lg + rr;
+        sm.nm[t][i] = i < t ? bt[rr] * fast_exp2(gt[rr] - gi_) * akk[n][rr] : 0.0f;
       }
     }
-  }
-  __syncthreads();
-
-  // ---- pack Aqk (bf16, fragment order; upper triangle zero) ----
-  uint16_t* frag = ws_frag + (static_cast<size_t>(r) * kVHeads + h) * 3 * kFragElems;
-  for (int qi = tid; qi < 512; qi += 256) {
-    const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
-    const int row = 16 * m + (l & 15);
-    const int dep = 32 * d + 8 * (l >> 4);
-    uint32_t w[4];
+    {
+      // aqk[n][rr] = K_i . Q_t (transposed), i = 16 ni + 4 lg + rr, t = 16 mi + l16
+      const int t = 16 * mi + l16;
+      const float gt = sm.lgam[t];
+      const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&sm.lgam[16 * ni + 4 * lg]);
+      float x[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i0 = dep + 2 * j, i1 = i0 + 1;
-      const float x0 = i0 <= row ? sm.tmat[row][i0] : 0.0f;
-      const float x1 = i1 <= row ? sm.tmat[row][i1] : 0.0f;
-      w[j] = pack_bf2(x0, x1);
-    }
-    *reinterpret_cast<uint4*>(frag + 2 * kFragElems + qi * 8) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-
-  // ---- K^T in fragment order (once per q/k head, by the even v-head) ----
-  if ((h & 1) == 0) {
-    uint16_t* kt = ws_kt + (static_cast<size_t>(r) * kQKHeads + hq) * kKTElems;
-    for (int qi = tid; qi < 1024; qi += 256) {
-      const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
-      const int kcol = 16 * m + (l & 15);
-      const int t = 32 * d + 8 * (l >> 4);
-      uint32_t w[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        w[j] = static_cast<uint32_t>(sm.kk[t + 2 * j][kcol]) |
-               (static_cast<uint32_t>(sm.kk[t + 2 * j + 1][kcol]) << 16);
-      *reinterpret_cast<uint4*>(kt + qi * 8) = make_uint4(w[0], w[1], w[2], w[3]);
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 16 * ni + 4 * lg + rr;
+        x[rr] = i <= t ? fast_exp2(gt - gi4[rr]) * aqk[n][rr] : 0.0f;
+      }
+      *reinterpret_cast<u32x2*>(frag + 2 * kFragElems + ((mi * 2 + (ni >> 1)) * 64 + lane) * 8 + 4 * (ni & 1)) =
+          u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
     }
   }
-  __syncthreads();   // Aqk consumed from tmat; tmat is free for T
+  // the six half-fragments of Aqk above the diagonal: (mi, ni) = (0,1) (0,2)
+  // (0,3) (1,2) (1,3) (2,3)
+  for (int z = tid; z < 6 * 64; z += kPrepassThreads) {
+    const int zj = z >> 6, zl = z & 63;
+    const int mi = zj < 3 ? 0 : (zj < 5 ? 1 : 2);
+    const int ni = zj < 3 ? zj + 1 : (zj < 5 ? zj - 1 : 3);
+    *reinterpret_cast<u32x2*>(frag + 2 * kFragElems + ((mi * 2 + (ni >> 1)) * 64 + zl) * 8 + 4 * (ni & 1)) =
+        u32x2{0u, 0u};
+  }
+  __syncthreads();   // N complete; K / Q space becomes T
 
   // ---- T = (I + N)^{-1}: diagonal 16x16 blocks by forward substitution ----
   if (lane < 16) {
-    const int base = 16 * wave;
+    const int base = 16 * w;
     const int j = lane;
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float acc = (i == j) ? 1.0f : 0.0f;
 #pragma unroll
-      for (int m2 = 0; m2 < i; ++m2) acc = fmaf(-sm.nmat[base + i][base + m2], x[m2], acc);
+      for (int m2 = 0; m2 < i; ++m2) acc = fmaf(-sm.nm[base + i][base + m2], x[m2], acc);
       x[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.tmat[base + i][base + j] = x[i];
+    for (int i = 0; i < 16; ++i) sm.u.tm[base + i][base + j] = x[i];
+  }
+
+  // ---- off-diagonal blocks by distance on fp32 MFMA:
+  //      T_ij = -T_ii P,  P = sum_{m=j}^{i-1} N_im T_mj  (P staged in N's unused upper block (j, i))
+#pragma unroll
+  for (int dist = 1; dist < 4; ++dist) {
+    __syncthreads();
+    if (w < 4 - dist) {
+      const int bj = w, bi = w + dist;
+      f32x4 p = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < dist; ++u)
+        p = block_prod(p, &sm.nm[16 * bi][16 * (bj + u)], &sm.u.tm[16 * (bj + u)][16 * bj], l16, lg);
+      float* scr = &sm.nm[16 * bj][16 * bi];
+      block_store(scr, p, 1.0f, l16, lg);
+      f32x4 tv = {0.f, 0.f, 0.f, 0.f};
+      tv = block_prod(tv, &sm.u.tm[16 * bi][16 * bi], scr, l16, lg);
+      block_store(&sm.u.tm[16 * bi][16 * bj], tv, -1.0f, l16, lg);
+    }
   }
   __syncthreads();
 
-  // ---- off-diagonal blocks: T_ij = -T_ii sum_{m=j}^{i-1} N_im T_mj, by distance ----
-  const int r0 = 4 * lg;
-  for (int dist = 1; dist < 4; ++dist) {
-    const bool active = wave < 4 - dist;
-    const int bj = wave, bi = wave + dist;
-    if (active) {
-      float p[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      for (int bm = bj; bm < bi; ++bm)
-        block_mma_acc(p, &sm.nmat[16 * bi][16 * bm], kMRow, &sm.tmat[16 * bm][16 * bj], kMRow,
-                      r0, l16);
-#pragma unroll
-      for (int aa = 0; aa < 4; ++aa) sm.pscr[wave][r0 + aa][l16] = p[aa];
-    }
-    __syncthreads();
-    if (active) {
-      float t4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      block_mma_acc(t4, &sm.tmat[16 * bi][16 * bi], kMRow, &sm.pscr[wave][0][0], 17, r0, l16);
-#pragma unroll
-      for (int aa = 0; aa < 4; ++aa) sm.tmat[16 * bi + r0 + aa][16 * bj + l16] = -t4[aa];
-    }
-    __syncthreads();
-  }
-
-  // ---- pack Tb = T diag(beta) as bf16 hi + lo (fragment order) ----
-  for (int qi = tid; qi < 512; qi += 256) {
+  // ---- pack Tb = T diag(beta) as bf16 hi + lo (permuted fragment order) ----
+  // fragment (m, d), lane l: row t = 16 m + l % 16, slots s: i = perm_depth(d, l / 16, s)
+  for (int qi = tid; qi < 512; qi += kPrepassThreads) {
     const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
-    const int row = 16 * m + (l & 15);
-    const int dep = 32 * d + 8 * (l >> 4);
-    uint32_t wh[4], wl[4];
+    const int t = 16 * m + (l & 15);
+    const int i0 = 32 * d + 4 * (l >> 4);
+    const f32x4 ta = *reinterpret_cast<const f32x4*>(&sm.u.tm[t][i0]);
+    const f32x4 tb = *reinterpret_cast<const f32x4*>(&sm.u.tm[t][i0 + 16]);
+    const f32x4 ba = *reinterpret_cast<const f32x4*>(&sm.beta[i0]);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(&sm.beta[i0 + 16]);
+    float x[8];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      x[s] = i0 + s <= t ? ta[s] * ba[s] : 0.0f;
+      x[4 + s] = i0 + 16 + s <= t ? tb[s] * bb[s] : 0.0f;
+    }
+    u32x4 wh, wl;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int i0 = dep + 2 * j, i1 = i0 + 1;
-      const float x0 = i0 <= row ? sm.tmat[row][i0] * sm.beta[i0] : 0.0f;
-      const float x1 = i1 <= row ? sm.tmat[row][i1] * sm.beta[i1] : 0.0f;
-      const uint16_t h0 = f2bf(x0), h1 = f2bf(x1);
-      wh[j] = static_cast<uint32_t>(h0) | (static_cast<uint32_t>(h1) << 16);
-      wl[j] = pack_bf2(x0 - bf2f(h0), x1 - bf2f(h1));
+      wh[j] = pack_bf2(x[2 * j], x[2 * j + 1]);
+      wl[j] = pack_bf2(x[2 * j] - bf_lo(wh[j]), x[2 * j + 1] - bf_hi(wh[j]));
     }
-    *reinterpret_cast<uint4*>(frag + qi * 8) = make_uint4(wh[0], wh[1], wh[2], wh[3]);
-    *reinterpret_cast<uint4*>(frag + kFragElems + qi * 8) = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+    *reinterpret_cast<u32x4*>(frag + qi * 8) = wh;
+    *reinterpret_cast<u32x4*>(frag + kFragElems + qi * 8) = wl;
   }
 }
 
 // ============================================================================
-// consumer: sequential chunk loop for one (seq, v-head, 16-wide V tile)
+// consumer: one work-group per (seq, v-head); wave w owns value rows 16w..16w+15
 // ============================================================================
-constexpr int kSRow = 136;    // bf16 per LDS row of S (v-major, k contiguous)
-constexpr int kTRow = 72;     // bf16 per LDS row of the [v][t] operands
+constexpr int kConsumerWaves = kDim / 16;  // 8: two waves per SIMD
+constexpr int kConsumerThreads = 64 * kConsumerWaves;
 
+// Chunk operands in LDS, double-buffered.  The buffer index is the outer index
+// of every field (not of a struct of fields) so that buffer 1 of a field sits
+// within a ds_read immediate offset of buffer 0.
+//   ks / qs : K / Q rows in natural column order; the 16-byte chunk j of row t
+//             is stored at position j ^ kq_swz(t), which makes the row reads
+//             (8 consecutive k) and the transposed reads (4 consecutive k of 4
+//             rows) bank-conflict free.
+//   vs      : V rows; chunk j of row t at j ^ v_swz(t).
+//   frag    : Tb hi, Tb lo, Aqk in permuted fragment order (lane-contiguous).
+//   gt      : gam[64], tail[64] and 128 floats of padding.
+// Rows t >= c of a partial chunk hold copies of row c-1 (finite data); they
+// only meet zero rows / columns of Tb and Aqk and zero gam / tail.
 struct __align__(16) ConsumerSmem {
-  // Wave-private staging of the chunk's K / Q rows (16 rows per wave, 16-byte
-  // k-chunks XOR-swizzled by row so fragment reads and row writes are both
-  // bank-conflict free) and of its V rows (16 rows x 16 values).
-  uint16_t kq[4][2][16][kDim];
-  uint16_t vs[4][16][kBV];
-  uint16_t s_bf[kBV][kSRow];      // S tile as bf16, [v][k]
-  uint16_t r_hi[kBV][kTRow];      // R = V - gam K S^T, [v][t]
-  uint16_t r_lo[kBV][kTRow];
-  uint16_t d_o[kBV][kTRow];       // Delta (bf16) for the output
-  uint16_t d_hi[kBV][kTRow];      // tail * Delta, hi / lo, for the state update
-  uint16_t d_lo[kBV][kTRow];
+  uint16_t ks[2][kChunk][kDim];
+  uint16_t qs[2][kChunk][kDim];
+  uint16_t vs[2][kChunk][kDim];
+  uint16_t frag[2][3][kFragElems];
+  float gt[2][4 * kChunk];
 };
 
-__device__ __forceinline__ bf16x8 gload_frag(const uint16_t* p) {
-  return *reinterpret_cast<const bf16x8*>(p);
+__device__ __forceinline__ int v_swz(int t) { return (t & 3) << 2; }
+
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// gfx950 transposed LDS read: in each 16-lane group, lane i receives element
+// (i & 3) of the 8-byte vectors addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
+__device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
 }
 
-__device__ __forceinline__ void split_store4(uint16_t* hi_dst, uint16_t* lo_dst, const float (&x)[4]) {
-  uint16_t hv[4];
-  float lv[4];
+__device__ __forceinline__ bf16x8 join_frag(u32x2 lo, u32x2 hi) {
+  return __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+}
+
+
+// Eight fp32 values in slot order -> bf16 fragment (hi) and the residual (lo).
+__device__ __forceinline__ void split_frag(const float (&x)[8], bf16x8& hi, bf16x8& lo) {
+  u32x4 h, l;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    hv[i] = f2bf(x[i]);
-    lv[i] = x[i] - bf2f(hv[i]);
+  for (int j = 0; j < 4; ++j) {
+    h[j] = pack_bf2(x[2 * j], x[2 * j + 1]);
+    l[j] = pack_bf2(x[2 * j] - bf_lo(h[j]), x[2 * j + 1] - bf_hi(h[j]));
   }
-  *reinterpret_cast<uint2*>(hi_dst) =
-      make_uint2(static_cast<uint32_t>(hv[0]) | (static_cast<uint32_t>(hv[1]) << 16),
-                 static_cast<uint32_t>(hv[2]) | (static_cast<uint32_t>(hv[3]) << 16));
-  *reinterpret_cast<uint2*>(lo_dst) = make_uint2(pack_bf2(lv[0], lv[1]), pack_bf2(lv[2], lv[3]));
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
 }
 
-__device__ __forceinline__ void store_bf4(uint16_t* dst, const float (&x)[4]) {
-  *reinterpret_cast<uint2*>(dst) = make_uint2(pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]));
+__device__ __forceinline__ bf16x8 round_frag(const float (&x)[8]) {
+  return __builtin_bit_cast(bf16x8, u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]),
+                                          pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])});
 }
 
-// Per-lane operands of one chunk step, loaded one chunk ahead so that the
-// global-memory latency overlaps the previous chunk's MFMA/LDS chain.
-struct ChunkOps {
-  u32x4 kr[4], qr[4];        // K, Q rows 16w + 4i + lane/16, 16-byte k-chunk lane%16
-  bf16x8 th[2], tl[2];       // Tb hi / lo fragments (rows 16w.., depth 32d..)
-  bf16x8 aq[2];              // Aqk fragments
-  bf16x8 kt[2][2];           // K^T fragments for k tiles 2w + i
-  f32x4 gam, tail;           // gam_t, tail_t for t = 16w + 4lg + rr
-  u32x2 vr;                  // V row 16w + lane/4, values v0 + 4(lane%4) .. +3
-  float gam_c;
-  int c;                     // chunk length
-  long long c0;              // first token
-};
+// The 8 slot values of permuted depth chunk d from four C-layout tiles
+// (tile 2d + s/4, row 4 lg + s%4).
+__device__ __forceinline__ void gather_slots(const f32x4 (&t)[4], int d, float (&x)[8]) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) x[s] = t[2 * d + (s >> 2)][s & 3];
+}
 
 // Where a chunk's operands live: first token, length, record index.
 struct ChunkRef {
@@ -426,300 +481,268 @@ struct ChunkRef {
   int rec;
 };
 
-// Operand loads of one chunk, in three parts issued at different points of the
-// previous steps so that the vector-memory pipe streams them while the MFMA
-// chain runs (issued as one burst they stall the issuing wave for thousands
-// of cycles).  Rows past the chunk end are clamped to the last valid row
-// instead of being masked: unconditional loads keep the prefetch free of wait
-// points, and the duplicate rows are harmless because gam, Tb and the V mask
-// zero R, Delta and every state contribution for t >= c, and their outputs are
-// never stored.
-template <int PART>
-__device__ __forceinline__ void load_chunk_part(
-    ChunkOps& o, const ChunkRef& r, int h, int hq, int v0, int w, int lane,
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const uint16_t* __restrict__ ws_frag,
-    const float* __restrict__ ws_gam, const uint16_t* __restrict__ ws_kt) {
-  const int l16 = lane & 15, lg = lane >> 4;
-  if constexpr (PART == 0) {
-    // 16 lanes read one 256-byte head row, so each load covers 4 whole rows
-    o.c0 = r.c0;
-    o.c = r.c;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = min(16 * w + 4 * i + lg, r.c - 1);
-      const size_t off = ((r.c0 + row) * kQKHeads + hq) * kDim + 8 * l16;
-      o.kr[i] = *reinterpret_cast<const u32x4*>(k + off);
-      o.qr[i] = *reinterpret_cast<const u32x4*>(q + off);
-    }
-    {
-      const int row = min(16 * w + (lane >> 2), r.c - 1);   // masked to 0 for t >= c where used
-      o.vr = *reinterpret_cast<const u32x2*>(v + ((r.c0 + row) * kVHeads + h) * kDim + v0 +
-                                             4 * (lane & 3));
-    }
-  } else if constexpr (PART == 1) {
-    const uint16_t* frag = ws_frag + (static_cast<size_t>(r.rec) * kVHeads + h) * 3 * kFragElems;
-    const float* gp = ws_gam + (static_cast<size_t>(r.rec) * kVHeads + h) * 2 * kChunk;
-#pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      const int fo = ((w * 2 + d) * 64 + lane) * 8;
-      o.th[d] = gload_frag(frag + fo);
-      o.tl[d] = gload_frag(frag + kFragElems + fo);
-    }
-    const int tb = 16 * w + 4 * lg;
-    o.gam = *reinterpret_cast<const f32x4*>(gp + tb);
-    o.tail = *reinterpret_cast<const f32x4*>(gp + kChunk + tb);
-    o.gam_c = gp[r.c - 1];
-  } else {
-    const uint16_t* frag = ws_frag + (static_cast<size_t>(r.rec) * kVHeads + h) * 3 * kFragElems;
-    const uint16_t* kt = ws_kt + (static_cast<size_t>(r.rec) * kQKHeads + hq) * kKTElems;
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-      o.aq[d] = gload_frag(frag + 2 * kFragElems + ((w * 2 + d) * 64 + lane) * 8);
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int d = 0; d < 2; ++d)
-        o.kt[i][d] = gload_frag(kt + (((2 * w + i) * 2 + d) * 64 + lane) * 8);
-  }
-}
-
-// Raw K / Q / V rows of a chunk -> this wave's LDS staging area.
-__device__ __forceinline__ void stage_rows(const ChunkOps& o, ConsumerSmem& sm, int w, int lane) {
-  const int l16 = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * i + lg;
-    *reinterpret_cast<u32x4*>(&sm.kq[w][0][row][8 * (l16 ^ row)]) = o.kr[i];
-    *reinterpret_cast<u32x4*>(&sm.kq[w][1][row][8 * (l16 ^ row)]) = o.qr[i];
-  }
-  *reinterpret_cast<u32x2*>(&sm.vs[w][lane >> 2][4 * (lane & 3)]) = o.vr;
-}
-
-// A fragment d (k = 32d + 8lg .. +7 of row l16) of the staged K (m = 0) or Q (m = 1).
-__device__ __forceinline__ bf16x8 staged_frag(const ConsumerSmem& sm, int w, int m, int d,
-                                              int l16, int lg) {
-  return *reinterpret_cast<const bf16x8*>(&sm.kq[w][m][l16][8 * ((4 * d + lg) ^ l16)]);
-}
-
-// Pointers and coordinates every chunk load of one consumer wave shares.
-struct LoadCtx {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  const uint16_t* ws_frag;
-  const float* ws_gam;
-  const uint16_t* ws_kt;
-  int h, hq, v0, w, lane;
+// Per-thread, chunk-invariant pieces of the operand copies.
+struct DmaLane {
+  int row;          // first K / Q / V row this lane copies (then +32 per pass)
+  uint32_t kq_col;   // byte offset of its K / Q source chunk inside the row
+  uint32_t v_col;    // byte offset of its V source chunk inside the row
 };
 
-template <int PART>
-__device__ __forceinline__ void load_part(ChunkOps& o, const ChunkRef& r, const LoadCtx& L) {
-  load_chunk_part<PART>(o, r, L.h, L.hq, L.v0, L.w, L.lane, L.q, L.k, L.v, L.ws_frag, L.ws_gam,
-                        L.ws_kt);
+// Issue the copies of one chunk's operands into buffer P.  The copies are
+// asynchronous; the barrier that ends the current chunk waits for them.
+template <int P>
+__device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, const DmaLane& dl,
+                                          int w, int lane, int h, int hq,
+                                          const uint16_t* __restrict__ q,
+                                          const uint16_t* __restrict__ k,
+                                          const uint16_t* __restrict__ v,
+                                          const uint16_t* __restrict__ ws_frag,
+                                          const float* __restrict__ ws_gam) {
+  const int cm1 = cr.c - 1;
+  const size_t qk0 = (static_cast<size_t>(cr.c0) * kQKHeads + hq) * kDim;
+  const char* kb = reinterpret_cast<const char*>(k + qk0);
+  const char* qb = reinterpret_cast<const char*>(q + qk0);
+  const char* vb = reinterpret_cast<const char*>(v + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim);
+  // each wave copies 4 rows (1 KB) per pass; 8 waves x 2 passes = 64 rows
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint32_t row = static_cast<uint32_t>(min(dl.row + 32 * j, cm1));
+    const uint32_t off = row * (kQKHeads * kDim * 2) + dl.kq_col;
+    dma16(kb + off, &sm.ks[P][32 * j + 4 * w][0]);
+    dma16(qb + off, &sm.qs[P][32 * j + 4 * w][0]);
+    dma16(vb + row * (kVHeads * kDim * 2) + dl.v_col, &sm.vs[P][32 * j + 4 * w][0]);
+  }
+  const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
+  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * 3 * kFragElems);
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    dma16(fb + (512 * j + 64 * w + lane) * 16, &sm.frag[P][0][0] + (512 * j + 64 * w) * 8);
+  if (w == 0)   // gam and tail are contiguous (512 bytes); lanes 32..63 fill the padding
+    dma16(reinterpret_cast<const char*>(ws_gam + rh * 2 * kChunk) + 16 * (lane & 31), &sm.gt[P][0]);
 }
 
-__device__ __forceinline__ void load_chunk_ops(ChunkOps& o, const ChunkRef& r, const LoadCtx& L) {
-  load_part<0>(o, r, L);
-  load_part<1>(o, r, L);
-  load_part<2>(o, r, L);
-}
+// One chunk of the recurrence for the 16-wide V tile of this wave.
+//   st : S^T tile in C layout with a k order chosen for the K row reads:
+//        st[kt][rr] = S[v0 + l16][kappa(kt, lg, rr)],
+//        kappa(kt, lg, rr) = 32 (kt >> 1) + 8 lg + 4 (kt & 1) + rr,
+//        so the 8 slots of depth chunk d, st[2d + s/4][s%4], are k = 32 d + 8 lg + s:
+//        one contiguous 16-byte piece of a K / Q row.
+//   orc : buffer resource over the chunk's output rows [c0, c0 + c) of this head
+//         (num_records = c rows, so stores of rows t >= c are dropped by the
+//         range check: no branch); ocol = byte offset of value column v0 + 4 lg.
+template <int P>
+__device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f32x4 (&st)[8], int w,
+                                               int lane, float scale, __amdgpu_buffer_rsrc_t orc,
+                                               uint32_t ocol) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  f32x4 gam[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) gam[m] = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
+  const float gam_c = sm.gt[P][c - 1];
 
-// One chunk step of the consumer for wave w: reads the state tile from LDS
-// (bf16) and its fp32 C-layout registers st, writes this chunk's outputs and
-// the advanced state.  Three work-group barriers.
-// The operands of chunk `pre` are loaded into `nxt` in three parts between
-// the stages; the raw rows of the following chunk (`mid`) replace this
-// chunk's in the wave's staging area once its fragments are in registers.
-__device__ __forceinline__ void consumer_step(const ChunkOps& cur, const ChunkOps& mid, ChunkOps& nxt,
-                                              const ChunkRef& pre,
-                                              const LoadCtx& L, f32x4 (&st)[2], ConsumerSmem& sm,
-                                              int h, int v0, int w, int l16, int lg, float scale,
-                                              uint16_t* __restrict__ out) {
-  const int c = cur.c;
-  const long long c0 = cur.c0;
-  // ---- stage 1: X = K S^T, Y = Q S^T for token rows 16w .. 16w+15 ----
-  f32x4 X = {0.f, 0.f, 0.f, 0.f}, Y = {0.f, 0.f, 0.f, 0.f};
-  bf16x8 ka[4], qa[4];
+  // ---- X = K S^T (rows t), Y^T = S Q^T (rows v); S as single bf16 ----
+  bf16x8 sb[4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    ka[d] = staged_frag(sm, w, 0, d, l16, lg);
-    qa[d] = staged_frag(sm, w, 1, d, l16, lg);
+    float x[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) x[s] = st[2 * d + (s >> 2)][s & 3];
+    sb[d] = round_frag(x);
   }
-  uint16_t vv[4];
+  const int rsw = kq_swz(l16);           // row t = 16 m + l16 has t & 15 == l16
+  f32x4 X[4], YT[4];
 #pragma unroll
-  for (int rr = 0; rr < 4; ++rr) vv[rr] = sm.vs[w][4 * lg + rr][l16];
+  for (int m = 0; m < 4; ++m) {
+    X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    const bf16x8 sb = lds_frag(&sm.s_bf[l16][32 * d + 8 * lg]);
-    X = mfma16(ka[d], sb, X);
-    Y = mfma16(qa[d], sb, Y);
-  }
-  stage_rows(mid, sm, w, L.lane);
-  load_part<0>(nxt, pre, L);
-
-  // ---- stage 2: R = V - gam X (hi/lo to LDS), Delta = Tb R ----
-  {
-    float rv[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const float vf = (16 * w + 4 * lg + rr < c) ? bf2f(vv[rr]) : 0.0f;
-      rv[rr] = vf - cur.gam[rr] * X[rr];
+    for (int d = 0; d < 4; ++d) {
+      const int at = 8 * ((4 * d + lg) ^ rsw);
+      const bf16x8 ka = *reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * m + l16][at]);
+      const bf16x8 qa = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][at]);
+      X[m] = mfma16(ka, sb[d], X[m]);
+      YT[m] = mfma16(sb[d], qa, YT[m]);
     }
-    split_store4(&sm.r_hi[l16][16 * w + 4 * lg], &sm.r_lo[l16][16 * w + 4 * lg], rv);
   }
-  __syncthreads();
-  f32x4 D = {0.f, 0.f, 0.f, 0.f};
+
+  // ---- R = V - gam X (V columns by transposed LDS reads), Delta = Tb R ----
+  // lane (lg, l16) addresses row 16m + 4lg + l16/4, columns 16w + 4(l16 & 3) .. +3
+  const int vrow = 4 * lg + (l16 >> 2);
+  const int vat = 8 * ((2 * w + ((l16 & 3) >> 1)) ^ v_swz(vrow)) + 4 * (l16 & 1);
+  f32x4 Rt[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const u32x2 vw = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
+    const float vv[4] = {bf_lo(vw.x), bf_hi(vw.x), bf_lo(vw.y), bf_hi(vw.y)};
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[m][rr] * X[m][rr];
+  }
+  bf16x8 rh[2], rl[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
-    const bf16x8 rh = lds_frag(&sm.r_hi[l16][32 * d + 8 * lg]);
-    const bf16x8 rl = lds_frag(&sm.r_lo[l16][32 * d + 8 * lg]);
-    D = mfma16(cur.th[d], rh, D);
-    D = mfma16(cur.th[d], rl, D);
-    D = mfma16(cur.tl[d], rh, D);
+    float x[8];
+    gather_slots(Rt, d, x);
+    split_frag(x, rh[d], rl[d]);
   }
-  load_part<1>(nxt, pre, L);
-
-  // ---- stage 3: Delta to LDS; O = scale (gam Y + Aqk Delta) ----
-  {
-    const float dv[4] = {D[0], D[1], D[2], D[3]};
-    float dt[4];
+  f32x4 D[4];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) dt[rr] = cur.tail[rr] * D[rr];
-    store_bf4(&sm.d_o[l16][16 * w + 4 * lg], dv);
-    split_store4(&sm.d_hi[l16][16 * w + 4 * lg], &sm.d_lo[l16][16 * w + 4 * lg], dt);
-  }
-  __syncthreads();
-  {
-    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < 4; ++m) {
+    D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-      const bf16x8 db = lds_frag(&sm.d_o[l16][32 * d + 8 * lg]);
-      O = mfma16(cur.aq[d], db, O);
-    }
-    load_part<2>(nxt, pre, L);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int t = 16 * w + 4 * lg + rr;
-      if (t < c) {
-        const float o = scale * (cur.gam[rr] * Y[rr] + O[rr]);
-        out[((c0 + t) * kVHeads + h) * kDim + v0 + l16] = f2bf(o);
-      }
+      const int fo = ((m * 2 + d) * 64 + lane) * 8;
+      const bf16x8 th = *reinterpret_cast<const bf16x8*>(&sm.frag[P][0][fo]);
+      const bf16x8 tl = *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][fo]);
+      D[m] = mfma16(th, rh[d], D[m]);
+      D[m] = mfma16(th, rl[d], D[m]);
+      D[m] = mfma16(tl, rh[d], D[m]);
     }
   }
 
-  // ---- stage 4: S^T <- gam_c S^T + K^T Delta' for this wave's k rows ----
+  // ---- Delta as bf16 (output) and Delta' = tail Delta as hi + lo (state) ----
+  bf16x8 dob[2], dh[2], dl[2];
+  {
+    f32x4 Dt[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    f32x4 acc = st[i] * cur.gam_c;
+    for (int m = 0; m < 4; ++m)
+      Dt[m] = D[m] * *reinterpret_cast<const f32x4*>(&sm.gt[P][kChunk + 16 * m + 4 * lg]);
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
-      const bf16x8 dh = lds_frag(&sm.d_hi[l16][32 * d + 8 * lg]);
-      const bf16x8 dl = lds_frag(&sm.d_lo[l16][32 * d + 8 * lg]);
-      acc = mfma16(cur.kt[i][d], dh, acc);
-      acc = mfma16(cur.kt[i][d], dl, acc);
+      float x[8];
+      gather_slots(D, d, x);
+      dob[d] = round_frag(x);
+      gather_slots(Dt, d, x);
+      split_frag(x, dh[d], dl[d]);
     }
-    st[i] = acc;
-    const float x[4] = {acc[0], acc[1], acc[2], acc[3]};
-    store_bf4(&sm.s_bf[l16][32 * w + 16 * i + 4 * lg], x);
   }
-  __syncthreads();
+
+  // ---- O^T = scale (Y^T diag(gam) + Delta^T Aqk^T): lane (lg, l16) holds token
+  //      16m + l16, value columns 4lg .. 4lg+3 -> one 8-byte store ----
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    f32x4 OT = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][2][((m * 2 + d) * 64 + lane) * 8]), OT);
+    const int t = 16 * m + l16;
+    const float sg = scale * sm.gt[P][t];
+    const u32x2 pk = {pack_bf2(sg * YT[m][0] + scale * OT[0], sg * YT[m][1] + scale * OT[1]),
+                      pack_bf2(sg * YT[m][2] + scale * OT[2], sg * YT[m][3] + scale * OT[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(pk, orc, static_cast<uint32_t>(t) * (kVHeads * kDim * 2) + ocol, 0, 0);
+  }
+
+  // ---- S^T <- gam_c S^T + K^T Delta' (K^T fragments by transposed reads) ----
+  // Tile kt, row i of the A operand is k = kappa(kt, i/4, i%4).  Lane sl of
+  // group lg addresses K[t][k0 .. k0+3], t = perm_depth(d, lg, sl/4) (+16 for
+  // slots 4..7), k0 = 32 (kt >> 1) + 8 (sl & 3) + 4 (kt & 1).
+  const int sl = l16;
+  const int tsw = kq_swz(4 * lg + (sl >> 2));   // t & 15 for both row sets
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt) {
+    f32x4 acc = st[kt] * gam_c;
+    const int at = 8 * ((4 * (kt >> 1) + (sl & 3)) ^ tsw) + 4 * (kt & 1);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int ta = perm_depth(d, lg, sl >> 2);
+      const u32x2 a0 = lds_tr16(&sm.ks[P][ta][at]);
+      const u32x2 a1 = lds_tr16(&sm.ks[P][ta + 16][at]);
+      const bf16x8 kta = join_frag(a0, a1);
+      acc = mfma16(kta, dh[d], acc);
+      acc = mfma16(kta, dl[d], acc);
+    }
+    st[kt] = acc;
+  }
 }
 
-// One work-group per CU by design (4 waves, one per SIMD): the register ring
-// of chunk operands needs the whole 512-entry VGPR+AGPR file of a SIMD.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void consumer_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, const float* __restrict__ state,
-    const void* __restrict__ cu, int is64, long long T, int R, float scale,
-    const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag,
-    const float* __restrict__ ws_gam, const uint16_t* __restrict__ ws_kt,
-    uint16_t* __restrict__ out, float* __restrict__ new_state) {
+// One work-group per CU by design: 146 KB of double-buffered chunk operands,
+// two waves per SIMD.
+__global__ __launch_bounds__(kConsumerThreads)
+void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                     const uint16_t* __restrict__ v, const float* __restrict__ state,
+                     const void* __restrict__ cu, int is64, long long T, int R, float scale,
+                     const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag,
+                     const float* __restrict__ ws_gam, uint16_t* __restrict__ out,
+                     float* __restrict__ new_state) {
   __shared__ ConsumerSmem sm;
-  // XCD-aware mapping: work-groups are dispatched round-robin over the 8 XCDs
-  // (XCD = linear id % 8).  The 8 V tiles of one (seq, v-head) read identical
-  // chunk operands, so they are given ids that are equal mod 8: they share one
-  // XCD's L2, and v-head h always lands on XCD h (where its prepass ran).
+  // XCD-aware mapping (XCD = linear id % 8): v-head h runs on XCD h, where its
+  // prepass records were written.
   const int bid = blockIdx.x;
-  const int grp = (bid / (kVHeads * kVTiles)) * kVHeads + (bid % kVHeads);   // s * 8 + h
-  const int vt = (bid / kVHeads) % kVTiles;
-  const int s = grp / kVHeads;
-  const int h = grp % kVHeads;
+  const int h = bid & 7;
+  const int s = bid >> 3;
   const int hq = h / kGva;
-  const int v0 = vt * kBV;
   const int tid = threadIdx.x;
-  const int w = tid >> 6;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
-  const int l16 = lane & 15;
-  const int lg = lane >> 4;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int vcol = 16 * w;                       // first value row of this wave's tile
 
   long long t0, t1;
   seq_bounds(cu, is64, s, T, t0, t1);
-
-  // State tile, transposed view S^T[k][v] in MFMA C layout: this wave owns
-  // k = 32w + 16i + 4lg + rr (i < 2, rr < 4) for v = v0 + l16.
-  float* ns_base = new_state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState +
-                   static_cast<size_t>(v0 + l16) * kDim;
+  // state tile in the kappa k order (see consumer_chunk)
+  const size_t st_off = ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim + 8 * lg;
+  auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
   if (t1 <= t0) {   // empty sequence: the reference leaves new_state zero
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<f32x4*>(ns_base + 32 * w + 16 * i + 4 * lg) = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < 8; ++kt)
+      *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = f32x4{0.f, 0.f, 0.f, 0.f};
     return;
   }
   const int rec0 = rec_start[s];
   const long long nchunks = (t1 - t0 + kChunk - 1) / kChunk;
   // chunks whose records exist (overlapping cu_seqlens can exhaust the capacity)
   const long long nvalid = rec0 >= R ? 0 : min(nchunks, static_cast<long long>(R - rec0));
-
-  const LoadCtx L{q, k, v, ws_frag, ws_gam, ws_kt, h, hq, v0, w, lane};
-  // chunk idx -> operand location; clamped to the last chunk so that the
-  // prefetch beyond the end re-reads valid data instead of being skipped
   auto chunk_ref = [&](long long idx) {
-    idx = min(idx, nvalid - 1);
     const long long c0 = t0 + idx * kChunk;
     return ChunkRef{c0, static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0)),
                     rec0 + static_cast<int>(idx)};
   };
-  ChunkOps bufA, bufB, bufC;
-  if (nvalid > 0) {
-    load_chunk_ops(bufA, chunk_ref(0), L);
-    load_chunk_ops(bufB, chunk_ref(1), L);
-    stage_rows(bufA, sm, w, lane);
-  }
-  f32x4 st[2];
-  if (state != nullptr) {
-    const float* s_base = state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState +
-                          static_cast<size_t>(v0 + l16) * kDim;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) st[i] = *reinterpret_cast<const f32x4*>(s_base + 32 * w + 16 * i + 4 * lg);
-  } else {
-    st[0] = st[1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const float x[4] = {st[i][0], st[i][1], st[i][2], st[i][3]};
-    store_bf4(&sm.s_bf[l16][32 * w + 16 * i + 4 * lg], x);
-  }
-  __syncthreads();
 
-  // Three operand buffers in a ring: chunk i + 2 is loading (spread over the
-  // stages of step i) while chunk i computes.  Every consumer_step call site
-  // sees the same loads in flight, so the compiler's wait counts never fall
-  // back to draining everything.
+  f32x4 st[8];
+  if (state != nullptr) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(state + st_off + kappa0(kt));
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  DmaLane dl;
+  {
+    const int r = 4 * w + (lane >> 4);     // + 32 j keeps r & 15
+    dl.row = r;
+    dl.kq_col = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(r));
+    dl.v_col = 16u * static_cast<uint32_t>((lane & 15) ^ v_swz(r));
+  }
+  const uint32_t ocol = 2u * static_cast<uint32_t>(vcol + 4 * lg);
+  auto out_rsrc = [&](const ChunkRef& cr) {
+    return __builtin_amdgcn_make_buffer_rsrc(out + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim, 0,
+                                             cr.c * (kVHeads * kDim * 2), 0x00020000);
+  };
+
   if (nvalid > 0) {
-    long long ci = 0;
-    for (;;) {
-      consumer_step(bufA, bufB, bufC, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
-      if (++ci >= nvalid) break;
-      consumer_step(bufB, bufC, bufA, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
-      if (++ci >= nvalid) break;
-      consumer_step(bufC, bufA, bufB, chunk_ref(ci + 2), L, st, sm, h, v0, w, l16, lg, scale, out);
-      if (++ci >= nvalid) break;
+    // Chunk i computes from buffer i & 1 while the copies of chunk i+1 into the
+    // other buffer are in flight; the barrier closing chunk i waits for them
+    // (and frees buffer i & 1 for chunk i+2).
+    dma_chunk<0>(sm, chunk_ref(0), dl, w, lane, h, hq, q, k, v, ws_frag, ws_gam);
+    __syncthreads();
+    for (long long i = 0; i < nvalid; i += 2) {
+      {
+        if (i + 1 < nvalid) dma_chunk<1>(sm, chunk_ref(i + 1), dl, w, lane, h, hq, q, k, v, ws_frag, ws_gam);
+        const ChunkRef cr = chunk_ref(i);
+        consumer_chunk<0>(sm, cr.c, st, w, lane, scale, out_rsrc(cr), ocol);
+        __syncthreads();
+      }
+      if (i + 1 < nvalid) {
+        if (i + 2 < nvalid) dma_chunk<0>(sm, chunk_ref(i + 2), dl, w, lane, h, hq, q, k, v, ws_frag, ws_gam);
+        const ChunkRef cr = chunk_ref(i + 1);
+        consumer_chunk<1>(sm, cr.c, st, w, lane, scale, out_rsrc(cr), ocol);
+        __syncthreads();
+      }
     }
   }
 
 #pragma unroll
-  for (int i = 0; i < 2; ++i) *reinterpret_cast<f32x4*>(ns_base + 32 * w + 16 * i + 4 * lg) = st[i];
+  for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = st[kt];
 }
 
 }  // namespace gdn
@@ -747,7 +770,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
   if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
   const long long R = max_records(num_seqs, total_tokens);
-  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * kVTiles > 0x7fffffffLL)
+  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads > 0x7fffffffLL)
     return GDN_ERR_INVALID_ARGUMENT;
   const WsLayout L = ws_layout(num_seqs, total_tokens);
   if (workspace_bytes < L.total) return GDN_ERR_WORKSPACE_TOO_SMALL;
@@ -756,7 +779,6 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   char* ws = static_cast<char*>(workspace);
   auto* frag = reinterpret_cast<uint16_t*>(ws + L.frag_off);
   auto* gam = reinterpret_cast<float*>(ws + L.gam_off);
-  auto* kt = reinterpret_cast<uint16_t*>(ws + L.kt_off);
   auto* rec_start = reinterpret_cast<int*>(ws + L.start_off);
   auto* recs = reinterpret_cast<int4*>(ws + L.rec_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -771,11 +793,10 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
                                                       total_tokens, static_cast<int>(R), rec_start,
                                                       recs);
   prepass_kernel<<<dim3(static_cast<unsigned>(R * kVHeads)), dim3(256), 0, st>>>(
-      qb, kb, A_log, ab, dt_bias, bb, recs, frag, gam, kt);
-  consumer_kernel<<<dim3(static_cast<unsigned>(num_seqs * kVHeads * kVTiles)), dim3(256), 0, st>>>(
+      qb, kb, A_log, ab, dt_bias, bb, recs, frag, gam);
+  consumer_kernel<<<dim3(static_cast<unsigned>(num_seqs) * kVHeads), dim3(kConsumerThreads), 0, st>>>(
       qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, static_cast<int>(R), scale,
-      rec_start, frag, gam,
-      kt, ob, new_state);
+      rec_start, frag, gam, ob, new_state);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
 }
