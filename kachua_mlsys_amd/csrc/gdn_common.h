@@ -17,6 +17,7 @@ constexpr int kDim = 128;                   // K == V == 128
 constexpr int kHeadState = kDim * kDim;     // floats per (seq, v-head) state tile
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
 typedef __attribute__((ext_vector_type(4))) float f32x4;
 // Native vectors for raw 16- / 8-byte payloads (HIP's uint4 / uint2 are union
 // structs that scalar replacement cannot split, which forces them to memory).
@@ -46,6 +47,13 @@ typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
 // with both operands; converting the halves one by one costs two plus a merge).
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
+
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+// Two fp32 -> packed fp16 pair, round-to-nearest-even (one v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
 }
 
 // ---- gate math (fp32, torch semantics) -------------------------------------

@@ -18,7 +18,7 @@
 //              sequences from cu_seqlens, with no host synchronisation.
 //   prepass  : one work-group per (record, v-head), all records in parallel:
 //              gates, K K^T / Q K^T on MFMA, fp32 blocked triangular inverse,
-//              and the packed MFMA operands Tb (bf16 hi+lo), Aqk (bf16) plus
+//              and the packed MFMA operands Tb (fp16), Aqk (bf16) plus
 //              gam / tail, written to the workspace.
 //   consumer : one work-group per (seq, v-head); each of its 8 waves (two per
 //              SIMD) owns one 16-wide V tile and runs the whole chunk
@@ -29,16 +29,19 @@
 //
 // Precision policy (fp32 accumulation everywhere): K, Q, V are bf16 inputs, so
 // their products are exact.  S enters K S^T and Q S^T as a single bf16; Tb and
-// R = V - gam K S^T enter Delta = Tb R as bf16 hi+lo pairs (three MFMAs); the
-// state update uses Delta' = tail Delta as a hi+lo pair; Aqk Delta (output only)
-// is single bf16.  The fp32 state never leaves registers between chunks.
+// R = V - gam K S^T enter Delta = Tb R as fp16 (11 significant bits: one MFMA
+// instead of three for a bf16 hi+lo pair); the state update uses
+// Delta' = tail Delta as a bf16 hi+lo pair; Aqk Delta (output only) is single
+// bf16.  The fp32 state never leaves registers between chunks.
 #include "gdn_common.h"
+#include <algorithm>
 #include "../../include/gdn_mi355x.h"
 
 namespace gdn {
 
 constexpr int kChunk = 64;
-constexpr int kFragElems = 4096;             // 64x64 bf16 operand in fragment order
+constexpr int kFragElems = 4096;             // 64x64 16-bit operand in fragment order
+constexpr int kFrags = 2;                    // per (record, v-head): Tb (fp16), Aqk (bf16)
 
 // MFMA operands in "permuted fragment order".  For v_mfma_f32_16x16x32_bf16
 // the hardware pairs slot s of lane group lg in A with the same slot of the
@@ -57,9 +60,10 @@ __host__ __device__ constexpr int perm_depth(int d, int lg, int s) {
 
 // ---- workspace layout -------------------------------------------------------
 struct WsLayout {
-  size_t frag_off;     // bf16 [R][8][3][4096]   (Tb hi, Tb lo, Aqk)
+  size_t frag_off;     // u16  [R][8][2][4096]   (Tb fp16, Aqk bf16)
   size_t gam_off;      // f32  [R][8][2][64]     (gam, tail)
   size_t start_off;    // i32  [N + 1]           record start per sequence
+  size_t list_off;     // i32  [2 + 2N]          counts (long, short), long list, short list
   size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
   size_t total;
 };
@@ -74,9 +78,10 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   WsLayout L;
   const size_t R = static_cast<size_t>(max_records(num_seqs, tokens));
   size_t off = 0;
-  L.frag_off = off;  off = align256(off + R * kVHeads * 3 * kFragElems * sizeof(uint16_t));
+  L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kFragElems * sizeof(uint16_t));
   L.gam_off = off;   off = align256(off + R * kVHeads * 2 * kChunk * sizeof(float));
   L.start_off = off; off = align256(off + (static_cast<size_t>(num_seqs) + 1) * sizeof(int));
+  L.list_off = off;  off = align256(off + (2 + 2 * static_cast<size_t>(num_seqs)) * sizeof(int));
   L.rec_off = off;   off = align256(off + R * sizeof(int4));
   L.total = off;
   return L;
@@ -104,34 +109,55 @@ __device__ __forceinline__ void seq_bounds(const void* cu, int is64, int s, long
 // ============================================================================
 constexpr int kPlanThreads = 1024;
 
+// Sequences of at least this many chunks run on the split consumer (chunk
+// time bounds the call); shorter ones on the full-head consumer (throughput).
+constexpr int kLongChunks = 2;
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
-    int* __restrict__ rec_start, int4* __restrict__ recs) {
-  __shared__ int part[kPlanThreads];
+    int* __restrict__ rec_start, int4* __restrict__ recs, int* __restrict__ lists) {
+  __shared__ int part[3][kPlanThreads];   // chunks, long sequences, short sequences
   const int tid = threadIdx.x;
   const int per = (num_seqs + kPlanThreads - 1) / kPlanThreads;
   const int s_begin = tid * per;
   const int s_end = min(num_seqs, s_begin + per);
-  int local = 0;
+  int local = 0, nlong = 0;
   for (int s = s_begin; s < s_end; ++s) {
     long long t0, t1;
     seq_bounds(cu, is64, s, T, t0, t1);
-    local += static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+    const long long nch = (t1 - t0 + kChunk - 1) / kChunk;
+    local += static_cast<int>(nch);
+    nlong += nch >= kLongChunks ? 1 : 0;
   }
-  part[tid] = local;
+  const int nshort = max(s_end - s_begin, 0) - nlong;
+  part[0][tid] = local;
+  part[1][tid] = nlong;
+  part[2][tid] = nshort;
   __syncthreads();
-  // Hillis-Steele inclusive scan over the per-thread totals
+  // Hillis-Steele inclusive scans over the per-thread totals
   for (int off = 1; off < kPlanThreads; off <<= 1) {
-    const int add = tid >= off ? part[tid - off] : 0;
+    int add[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) add[j] = tid >= off ? part[j][tid - off] : 0;
     __syncthreads();
-    part[tid] += add;
+#pragma unroll
+    for (int j = 0; j < 3; ++j) part[j][tid] += add[j];
     __syncthreads();
   }
-  int base = part[tid] - local;
-  const int total = min(part[kPlanThreads - 1], R);
+  int base = part[0][tid] - local;
+  int lpos = part[1][tid] - nlong, spos = part[2][tid] - nshort;
+  const int total = min(part[0][kPlanThreads - 1], R);
+  int* long_list = lists + 2;
+  int* short_list = lists + 2 + num_seqs;
+  if (tid == 0) {
+    lists[0] = part[1][kPlanThreads - 1];
+    lists[1] = part[2][kPlanThreads - 1];
+  }
   for (int s = s_begin; s < s_end; ++s) {
     long long t0, t1;
     seq_bounds(cu, is64, s, T, t0, t1);
+    if ((t1 - t0 + kChunk - 1) / kChunk >= kLongChunks) long_list[lpos++] = s;
+    else short_list[spos++] = s;
     rec_start[s] = base;
     // overlapping (non-monotonic) cu_seqlens can ask for more than R records:
     // records past the capacity are dropped and the consumer skips them
@@ -149,6 +175,10 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
 // ============================================================================
 __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16h(const f16x8& a, const f16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
@@ -280,7 +310,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
   // Q K^T is formed transposed (A = K rows, B = Q rows): lane (lg, l16) then
   // holds Aqk[16 mi + l16][16 ni + 4 lg + rr], which is exactly half (slots
   // 4 (ni & 1) .. +3) of fragment (mi, ni >> 1) in permuted fragment order.
-  uint16_t* frag = ws_frag + (static_cast<size_t>(r) * kVHeads + h) * 3 * kFragElems;
+  uint16_t* frag = ws_frag + (static_cast<size_t>(r) * kVHeads + h) * kFrags * kFragElems;
   const int rsw = kq_swz(l16);
   // wave w forms lower tiles j = w, w + 4, w + 8 (< 10) of both grams; all
   // twelve accumulator chains are independent, so their MFMAs interleave
@@ -329,7 +359,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
         const int i = 16 * ni + 4 * lg + rr;
         x[rr] = i <= t ? fast_exp2(gt - gi4[rr]) * aqk[n][rr] : 0.0f;
       }
-      *reinterpret_cast<u32x2*>(frag + 2 * kFragElems + ((mi * 2 + (ni >> 1)) * 64 + lane) * 8 + 4 * (ni & 1)) =
+      *reinterpret_cast<u32x2*>(frag + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + lane) * 8 + 4 * (ni & 1)) =
           u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
     }
   }
@@ -339,7 +369,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     const int zj = z >> 6, zl = z & 63;
     const int mi = zj < 3 ? 0 : (zj < 5 ? 1 : 2);
     const int ni = zj < 3 ? zj + 1 : (zj < 5 ? zj - 1 : 3);
-    *reinterpret_cast<u32x2*>(frag + 2 * kFragElems + ((mi * 2 + (ni >> 1)) * 64 + zl) * 8 + 4 * (ni & 1)) =
+    *reinterpret_cast<u32x2*>(frag + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + zl) * 8 + 4 * (ni & 1)) =
         u32x2{0u, 0u};
   }
   __syncthreads();   // N complete; K / Q space becomes T
@@ -380,7 +410,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
   }
   __syncthreads();
 
-  // ---- pack Tb = T diag(beta) as bf16 hi + lo (permuted fragment order) ----
+  // ---- pack Tb = T diag(beta) as fp16 (permuted fragment order) ----
   // fragment (m, d), lane l: row t = 16 m + l % 16, slots s: i = perm_depth(d, l / 16, s)
   for (int qi = tid; qi < 512; qi += kPrepassThreads) {
     const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
@@ -396,14 +426,8 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
       x[s] = i0 + s <= t ? ta[s] * ba[s] : 0.0f;
       x[4 + s] = i0 + 16 + s <= t ? tb[s] * bb[s] : 0.0f;
     }
-    u32x4 wh, wl;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      wh[j] = pack_bf2(x[2 * j], x[2 * j + 1]);
-      wl[j] = pack_bf2(x[2 * j] - bf_lo(wh[j]), x[2 * j + 1] - bf_hi(wh[j]));
-    }
-    *reinterpret_cast<u32x4*>(frag + qi * 8) = wh;
-    *reinterpret_cast<u32x4*>(frag + kFragElems + qi * 8) = wl;
+    *reinterpret_cast<u32x4*>(frag + qi * 8) =
+        u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
   }
 }
 
@@ -421,15 +445,15 @@ constexpr int kConsumerThreads = 64 * kConsumerWaves;
 //             (8 consecutive k) and the transposed reads (4 consecutive k of 4
 //             rows) bank-conflict free.
 //   vs      : V rows; chunk j of row t at j ^ v_swz(t).
-//   frag    : Tb hi, Tb lo, Aqk in permuted fragment order (lane-contiguous).
+//   frag    : Tb (fp16), Aqk (bf16) in permuted fragment order (lane-contiguous).
 //   gt      : gam[64], tail[64] and 128 floats of padding.
-// Rows t >= c of a partial chunk hold copies of row c-1 (finite data); they
-// only meet zero rows / columns of Tb and Aqk and zero gam / tail.
+// Rows t >= c of a partial chunk hold copies of row c-1 (finite data) or
+// zeros; they only meet zero rows / columns of Tb and Aqk and zero gam / tail.
 struct __align__(16) ConsumerSmem {
   uint16_t ks[2][kChunk][kDim];
   uint16_t qs[2][kChunk][kDim];
   uint16_t vs[2][kChunk][kDim];
-  uint16_t frag[2][3][kFragElems];
+  uint16_t frag[2][kFrags][kFragElems];
   float gt[2][4 * kChunk];
 };
 
@@ -460,6 +484,11 @@ __device__ __forceinline__ void split_frag(const float (&x)[8], bf16x8& hi, bf16
   }
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);
+}
+
+__device__ __forceinline__ f16x8 half_frag(const float (&x)[8]) {
+  return __builtin_bit_cast(f16x8, u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]),
+                                         pack_h2(x[4], x[5]), pack_h2(x[6], x[7])});
 }
 
 __device__ __forceinline__ bf16x8 round_frag(const float (&x)[8]) {
@@ -513,9 +542,9 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
     dma16(vb + row * (kVHeads * kDim * 2) + dl.v_col, &sm.vs[P][32 * j + 4 * w][0]);
   }
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
-  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * 3 * kFragElems);
+  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * kFrags * kFragElems);
 #pragma unroll
-  for (int j = 0; j < 3; ++j)
+  for (int j = 0; j < kFrags; ++j)
     dma16(fb + (512 * j + 64 * w + lane) * 16, &sm.frag[P][0][0] + (512 * j + 64 * w) * 8);
   if (w == 0)   // gam and tail are contiguous (512 bytes); lanes 32..63 fill the padding
     dma16(reinterpret_cast<const char*>(ws_gam + rh * 2 * kChunk) + 16 * (lane & 31), &sm.gt[P][0]);
@@ -577,26 +606,20 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[m][rr] * X[m][rr];
   }
-  bf16x8 rh[2], rl[2];
+  f16x8 rf[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
     float x[8];
     gather_slots(Rt, d, x);
-    split_frag(x, rh[d], rl[d]);
+    rf[d] = half_frag(x);
   }
   f32x4 D[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      const int fo = ((m * 2 + d) * 64 + lane) * 8;
-      const bf16x8 th = *reinterpret_cast<const bf16x8*>(&sm.frag[P][0][fo]);
-      const bf16x8 tl = *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][fo]);
-      D[m] = mfma16(th, rh[d], D[m]);
-      D[m] = mfma16(th, rl[d], D[m]);
-      D[m] = mfma16(tl, rh[d], D[m]);
-    }
+    for (int d = 0; d < 2; ++d)
+      D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][((m * 2 + d) * 64 + lane) * 8]), rf[d], D[m]);
   }
 
   // ---- Delta as bf16 (output) and Delta' = tail Delta as hi + lo (state) ----
@@ -623,7 +646,7 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
     f32x4 OT = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 2; ++d)
-      OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][2][((m * 2 + d) * 64 + lane) * 8]), OT);
+      OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][((m * 2 + d) * 64 + lane) * 8]), OT);
     const int t = 16 * m + l16;
     const float sg = scale * sm.gt[P][t];
     const u32x2 pk = {pack_bf2(sg * YT[m][0] + scale * OT[0], sg * YT[m][1] + scale * OT[1]),
@@ -654,21 +677,19 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
   }
 }
 
-// One work-group per CU by design: 146 KB of double-buffered chunk operands,
-// two waves per SIMD.
-__global__ __launch_bounds__(kConsumerThreads)
-void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                     const uint16_t* __restrict__ v, const float* __restrict__ state,
-                     const void* __restrict__ cu, int is64, long long T, int R, float scale,
-                     const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag,
-                     const float* __restrict__ ws_gam, uint16_t* __restrict__ out,
-                     float* __restrict__ new_state) {
-  __shared__ ConsumerSmem sm;
-  // XCD-aware mapping (XCD = linear id % 8): v-head h runs on XCD h, where its
-  // prepass records were written.
-  const int bid = blockIdx.x;
-  const int h = bid & 7;
-  const int s = bid >> 3;
+// Full-head consumer over the short-sequence list: work item = (list entry,
+// v-head), item i on work-group wg = i mod nwg.  nwg and the work-group's
+// linear id are multiples of 8 apart, so v-head h runs on XCD h (XCD = linear
+// id % 8), where its prepass records were written.
+__device__ __forceinline__ void full_head_items(
+    ConsumerSmem& sm, int wg, int nwg, const int* __restrict__ list, int nseq,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ state, const void* __restrict__ cu, int is64, long long T, int R, float scale,
+    const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
+    uint16_t* __restrict__ out, float* __restrict__ new_state) {
+  for (int item = wg; item < nseq * kVHeads; item += nwg) {
+  const int h = item & 7;
+  const int s = list[item >> 3];
   const int hq = h / kGva;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -685,7 +706,7 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
       *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = f32x4{0.f, 0.f, 0.f, 0.f};
-    return;
+    continue;
   }
   const int rec0 = rec_start[s];
   const long long nchunks = (t1 - t0 + kChunk - 1) / kChunk;
@@ -743,6 +764,382 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = st[kt];
+  }
+}
+
+// ============================================================================
+// split consumer: one work-group per (seq, v-head, half of the value rows)
+// ============================================================================
+// For sequences of several chunks the recurrence is a chain through the state,
+// so the time per chunk bounds the whole call.  Each 16-wide value tile gets
+// two waves on one SIMD: the chain wave (waves 0-3) carries the state through
+// X = K S^T, R, Delta = Tb R and S' = gam_c S + K^T Delta'; the side wave
+// (waves 4-7) forms the outputs (Y^T = S Q^T, O^T = Delta^T Aqk^T, stores) and
+// copies the next chunk's operands.  The chain wave hands S and Delta (bf16
+// fragments, in its own register order) to its side wave through LDS, so the
+// side wave's MFMAs and VALU work run in the gaps of the chain's dependent
+// MFMA sequence.  Two barriers per chunk: B2 (Delta ready; waits for LDS
+// traffic only, so the operand copies stay in flight) and B3 at the chunk's
+// end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
+// side wave reads them before B2 of chunk i+1, so one buffer suffices.
+constexpr int kSplitThreads = 512;
+constexpr int kConsumerGroups = 256;     // persistent work-groups per consumer kind (one per CU)
+constexpr int kHalfV = 64;                 // value rows per split work-group (4 tiles)
+
+struct __align__(16) SplitSmem {
+  uint16_t ks[2][kChunk][kDim];
+  uint16_t qs[2][kChunk][kDim];
+  uint16_t vs[2][kChunk][kHalfV];          // this half's value columns; chunk j of row t at j ^ vh_swz(t)
+  uint16_t frag[2][kFrags][kFragElems];
+  float gt[2][4 * kChunk];
+  u32x4 sbx[4][4][64];                     // chain wave w: bf16 S fragments sb[d], per lane
+  u32x4 dox[4][2][64];                     // chain wave w: bf16 Delta fragments dob[d], per lane
+};
+
+__device__ __forceinline__ int vh_swz(int t) { return ((t >> 1) & 1) << 2; }
+
+// Work-group barrier that waits for this wave's LDS operations only; its
+// global-to-LDS copies stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt / expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Buffer resource over [base, base + bytes): loads past the end return zeros
+// and stores past it are dropped by the hardware range check.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// 16 bytes per lane through a buffer resource straight into LDS (lane i of the
+// wave writes bytes [16 i, 16 i + 16) after the wave-uniform LDS address).
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, void* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
+                                           voff, 0, 0, 0);
+}
+
+// Per-lane byte offsets of the side-wave copies; chunk-invariant because each
+// chunk's base address lives in the (scalar) buffer resource.
+struct SplitDmaLane {
+  uint32_t kq[4];     // K / Q row (kr + 16 j), source chunk of this lane
+  uint32_t v[2];      // V row (vr + 32 j), this half's source chunk
+  uint32_t fr;        // fragment bytes of pass 0 (+4 KB per pass)
+  uint32_t g;         // gam / tail
+};
+
+__device__ __forceinline__ SplitDmaLane split_dma_lane(int ws, int lane, int hv) {
+  SplitDmaLane o;
+  const int kr = 4 * ws + (lane >> 4);    // + 16 j keeps kr & 15
+  const uint32_t kcol = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(kr));
+#pragma unroll
+  for (int j = 0; j < 4; ++j) o.kq[j] = static_cast<uint32_t>(kr + 16 * j) * (kQKHeads * kDim * 2) + kcol;
+  const int vr = 8 * ws + (lane >> 3);    // + 32 j keeps vr & 3
+  const uint32_t vcol = 2u * kHalfV * hv + 16u * static_cast<uint32_t>((lane & 7) ^ vh_swz(vr));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) o.v[j] = static_cast<uint32_t>(vr + 32 * j) * (kVHeads * kDim * 2) + vcol;
+  o.fr = static_cast<uint32_t>(64 * ws + lane) * 16u;
+  o.g = 16u * static_cast<uint32_t>(lane & 31);
+  return o;
+}
+
+// Side-wave copies of one chunk's operands into buffer P (4 side waves).
+// Rows t >= c fall outside the K / Q / V resources and arrive as zeros.
+template <int P>
+__device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, const SplitDmaLane& dl, int ws,
+                                          int h, int hq, const uint16_t* __restrict__ q,
+                                          const uint16_t* __restrict__ k,
+                                          const uint16_t* __restrict__ v,
+                                          const uint16_t* __restrict__ ws_frag,
+                                          const float* __restrict__ ws_gam) {
+  const size_t qk0 = (static_cast<size_t>(cr.c0) * kQKHeads + hq) * kDim;
+  const uint32_t kq_bytes = static_cast<uint32_t>(cr.c) * (kQKHeads * kDim * 2);
+  const __amdgpu_buffer_rsrc_t kr = buf_rsrc(k + qk0, kq_bytes);
+  const __amdgpu_buffer_rsrc_t qr = buf_rsrc(q + qk0, kq_bytes);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    dma16_buf(kr, dl.kq[j], &sm.ks[P][16 * j + 4 * ws][0]);
+    dma16_buf(qr, dl.kq[j], &sm.qs[P][16 * j + 4 * ws][0]);
+  }
+  const __amdgpu_buffer_rsrc_t vr = buf_rsrc(v + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
+                                             static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
+#pragma unroll
+  for (int j = 0; j < 2; ++j) dma16_buf(vr, dl.v[j], &sm.vs[P][32 * j + 8 * ws][0]);
+  const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
+  const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kFrags * kFragElems, kFrags * kFragElems * 2);
+#pragma unroll
+  for (int j = 0; j < 2 * kFrags; ++j) dma16_buf(fr, dl.fr + 4096u * j, &sm.frag[P][0][0] + (256 * j + 64 * ws) * 8);
+  if (ws == 0) dma16_buf(buf_rsrc(ws_gam + rh * 2 * kChunk, 2 * kChunk * 4), dl.g, &sm.gt[P][0]);
+}
+
+// bf16 B-operand fragments of the state tile: slots of depth chunk d are
+// st[2d + s/4][s%4] (k = 32 d + 8 lg + s in the kappa order).
+__device__ __forceinline__ void state_frags(const f32x4 (&st)[8], bf16x8 (&sb)[4]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float x[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) x[s] = st[2 * d + (s >> 2)][s & 3];
+    sb[d] = round_frag(x);
+  }
+}
+
+// Chain wave, one chunk: S^T tile st (kappa k order, as in consumer_chunk).
+template <int P>
+__device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8], int w, int lane) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  bf16x8 sb[4];
+  state_frags(st, sb);
+
+  // ---- X = K S^T ----
+  const int rsw = kq_swz(l16);
+  f32x4 X[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      X[m] = mfma16(*reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]),
+                    sb[d], X[m]);
+  }
+  // ---- R = V - gam X, Delta = Tb R (fp16) ----
+  const int vrow = 4 * lg + (l16 >> 2);
+  const int vat = 8 * ((2 * w + ((l16 & 3) >> 1)) ^ vh_swz(vrow)) + 4 * (l16 & 1);
+  f32x4 Rt[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const f32x4 gam = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
+    const u32x2 vw = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
+    const float vv[4] = {bf_lo(vw.x), bf_hi(vw.x), bf_lo(vw.y), bf_hi(vw.y)};
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[rr] * X[m][rr];
+  }
+  f16x8 rf[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    float x[8];
+    gather_slots(Rt, d, x);
+    rf[d] = half_frag(x);
+  }
+  f32x4 D[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][((m * 2 + d) * 64 + lane) * 8]), rf[d], D[m]);
+  }
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    float x[8];
+    gather_slots(D, d, x);
+    sm.dox[w][d][lane] = __builtin_bit_cast(u32x4, round_frag(x));
+  }
+  lds_barrier();   // B2: Delta fragments visible to the side wave (and S fragments consumed)
+
+  // ---- Delta' = tail Delta (hi + lo); S^T <- gam_c S^T + K^T Delta' ----
+  bf16x8 dh[2], dl[2];
+  {
+    f32x4 Dt[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Dt[m] = D[m] * *reinterpret_cast<const f32x4*>(&sm.gt[P][kChunk + 16 * m + 4 * lg]);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      float x[8];
+      gather_slots(Dt, d, x);
+      split_frag(x, dh[d], dl[d]);
+    }
+  }
+  const float gam_c = sm.gt[P][c - 1];
+  // K^T fragments: tile kt, row i of the A operand is k = kappa(kt, i/4, i%4);
+  // lane sl of group lg addresses K[t][k0 .. k0+3], t = perm_depth(d, lg, sl/4)
+  // (+16 for slots 4..7), k0 = 32 (kt >> 1) + 8 (sl & 3) + 4 (kt & 1).
+  const int sl = l16;
+  const int tsw = kq_swz(4 * lg + (sl >> 2));
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt) {
+    f32x4 acc = st[kt] * gam_c;
+    const int at = 8 * ((4 * (kt >> 1) + (sl & 3)) ^ tsw) + 4 * (kt & 1);
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const int ta = perm_depth(d, lg, sl >> 2);
+      const bf16x8 kta = join_frag(lds_tr16(&sm.ks[P][ta][at]), lds_tr16(&sm.ks[P][ta + 16][at]));
+      acc = mfma16(kta, dh[d], acc);
+      acc = mfma16(kta, dl[d], acc);
+    }
+    st[kt] = acc;
+  }
+  // S fragments of the next chunk for the side wave (read before its next B2)
+  bf16x8 nb[4];
+  state_frags(st, nb);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) sm.sbx[w][d][lane] = __builtin_bit_cast(u32x4, nb[d]);
+}
+
+// Side wave, one chunk: outputs of the chunk (tile of chain wave ws).
+template <int P, typename Copy>
+__device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, float scale,
+                                           __amdgpu_buffer_rsrc_t orc, uint32_t ocol, Copy&& copy_next) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int rsw = kq_swz(l16);
+  bf16x8 sb[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) sb[d] = __builtin_bit_cast(bf16x8, sm.sbx[ws][d][lane]);
+  f32x4 YT[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      YT[m] = mfma16(sb[d], *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]),
+                     YT[m]);
+  }
+  copy_next();     // next chunk's operands, in flight until B3
+  lds_barrier();   // B2
+  bf16x8 dob[2];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) dob[d] = __builtin_bit_cast(bf16x8, sm.dox[ws][d][lane]);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    f32x4 OT = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][((m * 2 + d) * 64 + lane) * 8]), OT);
+    const int t = 16 * m + l16;
+    const float sg = scale * sm.gt[P][t];
+    const u32x2 pk = {pack_bf2(sg * YT[m][0] + scale * OT[0], sg * YT[m][1] + scale * OT[1]),
+                      pack_bf2(sg * YT[m][2] + scale * OT[2], sg * YT[m][3] + scale * OT[3])};
+    __builtin_amdgcn_raw_buffer_store_b64(pk, orc, static_cast<uint32_t>(t) * (kVHeads * kDim * 2) + ocol, 0, 0);
+  }
+}
+
+// Split consumer over the long-sequence list: work item = (list entry, half,
+// v-head) as entry * 16 + half * 8 + h, item i on work-group wg = i mod nwg
+// (multiples of 8 apart: v-head h runs on XCD h, both halves share its L2).
+__device__ __forceinline__ void split_items(
+    SplitSmem& sm, int wg, int nwg, const int* __restrict__ list, int nseq,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ state, const void* __restrict__ cu, int is64, long long T, int R, float scale,
+    const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
+    uint16_t* __restrict__ out, float* __restrict__ new_state) {
+  for (int item = wg; item < nseq * 2 * kVHeads; item += nwg) {
+  const int h = item & 7;
+  const int hv = (item >> 3) & 1;
+  const int s = list[item >> 4];
+  const int hq = h / kGva;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool chain = w < 4;
+  const int wt = w & 3;                          // value tile of this wave pair
+  const int lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int vcol = kHalfV * hv + 16 * wt;
+
+  long long t0, t1;
+  seq_bounds(cu, is64, s, T, t0, t1);
+  const size_t st_off = ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim + 8 * lg;
+  auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
+  if (t1 <= t0) {   // empty sequence: the reference leaves new_state zero
+    if (chain) {
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt)
+        *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    continue;
+  }
+  const int rec0 = rec_start[s];
+  const long long nchunks = (t1 - t0 + kChunk - 1) / kChunk;
+  const long long nvalid = rec0 >= R ? 0 : min(nchunks, static_cast<long long>(R - rec0));
+  auto chunk_ref = [&](long long idx) {
+    const long long c0 = t0 + idx * kChunk;
+    return ChunkRef{c0, static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0)),
+                    rec0 + static_cast<int>(idx)};
+  };
+
+  f32x4 st[8];
+  if (chain && state != nullptr) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(state + st_off + kappa0(kt));
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  const uint32_t ocol = 2u * static_cast<uint32_t>(vcol + 4 * lg);
+  auto out_rsrc = [&](const ChunkRef& cr) {
+    return buf_rsrc(out + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
+                    static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
+  };
+  const SplitDmaLane dl = split_dma_lane(wt, lane, hv);
+
+  if (nvalid > 0) {
+    if (chain) {
+      bf16x8 sb[4];
+      state_frags(st, sb);
+#pragma unroll
+      for (int d = 0; d < 4; ++d) sm.sbx[wt][d][lane] = __builtin_bit_cast(u32x4, sb[d]);
+    } else {
+      split_dma<0>(sm, chunk_ref(0), dl, wt, h, hq, q, k, v, ws_frag, ws_gam);
+    }
+    __syncthreads();
+    for (long long i = 0; i < nvalid; i += 2) {
+      {
+        const ChunkRef cr = chunk_ref(i);
+        if (chain) {
+          chain_chunk<0>(sm, cr.c, st, wt, lane);
+        } else {
+          side_chunk<0>(sm, wt, lane, scale, out_rsrc(cr), ocol, [&] {
+            if (i + 1 < nvalid) split_dma<1>(sm, chunk_ref(i + 1), dl, wt, h, hq, q, k, v, ws_frag, ws_gam);
+          });
+        }
+        __syncthreads();   // B3: buffer 0 free, buffer 1 landed
+      }
+      if (i + 1 < nvalid) {
+        const ChunkRef cr = chunk_ref(i + 1);
+        if (chain) {
+          chain_chunk<1>(sm, cr.c, st, wt, lane);
+        } else {
+          side_chunk<1>(sm, wt, lane, scale, out_rsrc(cr), ocol, [&] {
+            if (i + 2 < nvalid) split_dma<0>(sm, chunk_ref(i + 2), dl, wt, h, hq, q, k, v, ws_frag, ws_gam);
+          });
+        }
+        __syncthreads();
+      }
+    }
+  }
+
+  if (chain) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = st[kt];
+  }
+  }
+}
+
+// Consumer entry: work-groups [0, g_long) run the split consumer over the
+// long-sequence list, the rest the full-head consumer over the short list, so
+// both regimes of a mixed batch run concurrently.  Lists come from plan_kernel
+// (no host synchronisation); an empty list costs one short round of groups.
+union ConsumerLds {
+  ConsumerSmem full;
+  SplitSmem split;
+};
+
+__global__ __launch_bounds__(kSplitThreads)
+void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                     const uint16_t* __restrict__ v, const float* __restrict__ state,
+                     const void* __restrict__ cu, int is64, long long T, int R, float scale,
+                     const int* __restrict__ rec_start, const int* __restrict__ lists, int num_seqs,
+                     int g_long, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
+                     uint16_t* __restrict__ out, float* __restrict__ new_state) {
+  __shared__ ConsumerLds sm;
+  const int bid = blockIdx.x;
+  if (bid < g_long) {
+    split_items(sm.split, bid, g_long, lists + 2, lists[0], q, k, v, state, cu, is64, T, R, scale, rec_start,
+                ws_frag, ws_gam, out, new_state);
+  } else {
+    full_head_items(sm.full, bid - g_long, static_cast<int>(gridDim.x) - g_long, lists + 2 + num_seqs, lists[1],
+                    q, k, v, state, cu, is64, T, R, scale, rec_start, ws_frag, ws_gam, out, new_state);
+  }
 }
 
 }  // namespace gdn
@@ -770,7 +1167,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
   if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
   const long long R = max_records(num_seqs, total_tokens);
-  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads > 0x7fffffffLL)
+  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * 2 > 0x7fffffffLL)
     return GDN_ERR_INVALID_ARGUMENT;
   const WsLayout L = ws_layout(num_seqs, total_tokens);
   if (workspace_bytes < L.total) return GDN_ERR_WORKSPACE_TOO_SMALL;
@@ -780,6 +1177,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   auto* frag = reinterpret_cast<uint16_t*>(ws + L.frag_off);
   auto* gam = reinterpret_cast<float*>(ws + L.gam_off);
   auto* rec_start = reinterpret_cast<int*>(ws + L.start_off);
+  auto* lists = reinterpret_cast<int*>(ws + L.list_off);
   auto* recs = reinterpret_cast<int4*>(ws + L.rec_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const auto* qb = static_cast<const uint16_t*>(q);
@@ -791,12 +1189,15 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
 
   plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                       total_tokens, static_cast<int>(R), rec_start,
-                                                      recs);
+                                                      recs, lists);
   prepass_kernel<<<dim3(static_cast<unsigned>(R * kVHeads)), dim3(256), 0, st>>>(
       qb, kb, A_log, ab, dt_bias, bb, recs, frag, gam);
-  consumer_kernel<<<dim3(static_cast<unsigned>(num_seqs) * kVHeads), dim3(kConsumerThreads), 0, st>>>(
+  // persistent grids: one work-group per CU per consumer kind at most
+  const long long g_long = std::min<long long>(static_cast<long long>(num_seqs) * 2 * kVHeads, kConsumerGroups);
+  const long long g_short = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads, kConsumerGroups);
+  consumer_kernel<<<dim3(static_cast<unsigned>(g_long + g_short)), dim3(kSplitThreads), 0, st>>>(
       qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, static_cast<int>(R), scale,
-      rec_start, frag, gam, ob, new_state);
+      rec_start, lists, num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
 }
