@@ -113,10 +113,28 @@ constexpr int kPlanThreads = 1024;
 // time bounds the call); shorter ones on the full-head consumer (throughput).
 constexpr int kLongChunks = 2;
 
+// Inclusive prefix sum over the NT threads of the work-group: shuffle scan
+// inside each wave, then one pass over the wave totals (wave_tot: NT / 64 ints).
+template <int NT>
+__device__ __forceinline__ int block_scan(int x, int* wave_tot) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(x, off, 64);
+    if (lane >= off) x += o;
+  }
+  if (lane == 63) wave_tot[wv] = x;
+  __syncthreads();
+  int add = 0;
+  for (int j = 0; j < wv; ++j) add += wave_tot[j];
+  __syncthreads();
+  return x + add;
+}
+
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
     int* __restrict__ rec_start, int4* __restrict__ recs, int* __restrict__ lists) {
-  __shared__ int part[3][kPlanThreads];   // chunks, long sequences, short sequences
+  __shared__ int wave_tot[3][kPlanThreads / 64];
   const int tid = threadIdx.x;
   const int per = (num_seqs + kPlanThreads - 1) / kPlanThreads;
   const int s_begin = tid * per;
@@ -130,28 +148,23 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     nlong += nch >= kLongChunks ? 1 : 0;
   }
   const int nshort = max(s_end - s_begin, 0) - nlong;
-  part[0][tid] = local;
-  part[1][tid] = nlong;
-  part[2][tid] = nshort;
-  __syncthreads();
-  // Hillis-Steele inclusive scans over the per-thread totals
-  for (int off = 1; off < kPlanThreads; off <<= 1) {
-    int add[3];
-#pragma unroll
-    for (int j = 0; j < 3; ++j) add[j] = tid >= off ? part[j][tid - off] : 0;
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 3; ++j) part[j][tid] += add[j];
-    __syncthreads();
+  const int inc_c = block_scan<kPlanThreads>(local, wave_tot[0]);
+  const int inc_l = block_scan<kPlanThreads>(nlong, wave_tot[1]);
+  const int inc_s = block_scan<kPlanThreads>(nshort, wave_tot[2]);
+  int base = inc_c - local;
+  int lpos = inc_l - nlong, spos = inc_s - nshort;
+  int total_c = 0, total_l = 0, total_s = 0;
+  for (int j = 0; j < kPlanThreads / 64; ++j) {
+    total_c += wave_tot[0][j];
+    total_l += wave_tot[1][j];
+    total_s += wave_tot[2][j];
   }
-  int base = part[0][tid] - local;
-  int lpos = part[1][tid] - nlong, spos = part[2][tid] - nshort;
-  const int total = min(part[0][kPlanThreads - 1], R);
+  const int total = min(total_c, R);
   int* long_list = lists + 2;
   int* short_list = lists + 2 + num_seqs;
   if (tid == 0) {
-    lists[0] = part[1][kPlanThreads - 1];
-    lists[1] = part[2][kPlanThreads - 1];
+    lists[0] = total_l;
+    lists[1] = total_s;
   }
   for (int s = s_begin; s < s_end; ++s) {
     long long t0, t1;
@@ -236,21 +249,104 @@ __device__ __forceinline__ void block_store(float* Z, const f32x4& v, float sc, 
   for (int rr = 0; rr < 4; ++rr) Z[(4 * lg + rr) * kMRow + l16] = sc * v[rr];
 }
 
+// Record r of a batch of at most kFusedPlanSeqs sequences (one per thread),
+// found by the work-group itself (no plan launch): exclusive scan of
+// per-sequence chunk counts; the thread owning the sequence that contains r
+// publishes it.  The
+// work-group of record 0, v-head 0 also writes rec_start and the long / short
+// sequence lists for the consumer, as plan_kernel does.  Returns false when
+// record r does not exist.
+constexpr int kFusedPlanSeqs = 256;   // larger batches: the scan per work-group costs more than a launch
+
+__device__ bool find_record(int r, bool bookkeeping, const void* __restrict__ cu, int is64, int num_seqs,
+                            long long T, int R, int* __restrict__ rec_start, int* __restrict__ lists,
+                            int* scratch, long long& t0_out, int& c_out) {
+  const int tid = threadIdx.x;
+  const int per = (num_seqs + kPrepassThreads - 1) / kPrepassThreads;
+  const int s_begin = tid * per;
+  const int s_end = min(num_seqs, s_begin + per);
+  int local = 0, nlong = 0;
+  for (int s = s_begin; s < s_end; ++s) {
+    long long t0, t1;
+    seq_bounds(cu, is64, s, T, t0, t1);
+    const long long nch = (t1 - t0 + kChunk - 1) / kChunk;
+    local += static_cast<int>(nch);
+    nlong += nch >= kLongChunks ? 1 : 0;
+  }
+  if (tid == 0) scratch[0] = -1;
+  const int inc = block_scan<kPrepassThreads>(local, scratch + 8);
+  int base = inc - local;
+  int total = 0;
+  for (int j = 0; j < kPrepassThreads / 64; ++j) total += scratch[8 + j];
+  int lpos = 0, spos = 0;
+  if (bookkeeping) {
+    const int nshort = max(s_end - s_begin, 0) - nlong;
+    const int inc_l = block_scan<kPrepassThreads>(nlong, scratch + 16);
+    const int inc_s = block_scan<kPrepassThreads>(nshort, scratch + 24);
+    lpos = inc_l - nlong;
+    spos = inc_s - nshort;
+    if (tid == 0) {
+      int tl = 0, ts = 0;
+      for (int j = 0; j < kPrepassThreads / 64; ++j) {
+        tl += scratch[16 + j];
+        ts += scratch[24 + j];
+      }
+      lists[0] = tl;
+      lists[1] = ts;
+      rec_start[num_seqs] = min(total, R);
+    }
+  }
+  for (int s = s_begin; s < s_end; ++s) {
+    long long t0, t1;
+    seq_bounds(cu, is64, s, T, t0, t1);
+    const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+    if (r >= base && r < base + nch) {
+      scratch[0] = s;
+      scratch[1] = r - base;
+    }
+    if (bookkeeping) {
+      rec_start[s] = base;
+      if (nch >= kLongChunks) lists[2 + lpos++] = s;
+      else lists[2 + num_seqs + spos++] = s;
+    }
+    base += nch;
+  }
+  __syncthreads();
+  const int s = scratch[0];
+  if (s < 0) return false;
+  long long t0, t1;
+  seq_bounds(cu, is64, s, T, t0, t1);
+  t0_out = t0 + static_cast<long long>(scratch[1]) * kChunk;
+  c_out = static_cast<int>(min(static_cast<long long>(kChunk), t1 - t0_out));
+  return true;
+}
+
 __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
-    const int4* __restrict__ recs, uint16_t* __restrict__ ws_frag,
-    float* __restrict__ ws_gam) {
+    const int4* __restrict__ recs, const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
+    int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
+    uint16_t* __restrict__ ws_frag, float* __restrict__ ws_gam) {
   __shared__ PrepassSmem sm;
   // linear id = r * 8 + h: v-head h runs on XCD h, as its consumer does
   const int r = blockIdx.x / kVHeads;
   const int h = blockIdx.x % kVHeads;
   const int hq = h / kGva;
-  const int4 rec = recs[r];
-  const int c = rec.z;
-  if (c <= 0) return;
-  const long long t0 = rec.y;
+  int c;
+  long long t0;
+  if (fused_plan) {
+    // N's space is free until the grams; it holds the record search scratch
+    if (!find_record(r, blockIdx.x == 0, cu, is64, num_seqs, T, R, rec_start, lists,
+                     reinterpret_cast<int*>(&sm.nm[0][0]), t0, c))
+      return;
+    __syncthreads();   // scratch read by every thread before N is written
+  } else {
+    const int4 rec = recs[r];
+    c = rec.z;
+    if (c <= 0) return;
+    t0 = rec.y;
+  }
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -1187,11 +1283,16 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   const auto* bb = static_cast<const uint16_t*>(b);
   auto* ob = static_cast<uint16_t*>(output);
 
-  plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
-                                                      total_tokens, static_cast<int>(R), rec_start,
-                                                      recs, lists);
-  prepass_kernel<<<dim3(static_cast<unsigned>(R * kVHeads)), dim3(256), 0, st>>>(
-      qb, kb, A_log, ab, dt_bias, bb, recs, frag, gam);
+  // small batches: every prepass work-group finds its own record (one launch
+  // fewer); large ones: a separate plan launch numbers the records once
+  const int fused_plan = num_seqs <= kFusedPlanSeqs ? 1 : 0;
+  if (!fused_plan)
+    plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
+                                                        total_tokens, static_cast<int>(R), rec_start,
+                                                        recs, lists);
+  prepass_kernel<<<dim3(static_cast<unsigned>(R * kVHeads)), dim3(kPrepassThreads), 0, st>>>(
+      qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
+      static_cast<int>(R), fused_plan, rec_start, lists, frag, gam);
   // persistent grids: one work-group per CU per consumer kind at most
   const long long g_long = std::min<long long>(static_cast<long long>(num_seqs) * 2 * kVHeads, kConsumerGroups);
   const long long g_short = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads, kConsumerGroups);
