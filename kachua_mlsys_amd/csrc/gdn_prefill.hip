@@ -875,8 +875,8 @@ __device__ __forceinline__ void full_head_items(
 // fragments, in its own register order) to its side wave through LDS, so the
 // side wave's MFMAs and VALU work run in the gaps of the chain's dependent
 // MFMA sequence.  Two barriers per chunk: B2 (Delta ready; waits for LDS
-// traffic only, so the operand copies stay in flight) and B3 at the chunk's
-// end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
+// traffic only, so the operand copies, issued at the chunk's start, stay in
+// flight) and B3 at the chunk's end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
 // side wave reads them before B2 of chunk i+1, so one buffer suffices.
 constexpr int kSplitThreads = 512;
 constexpr int kConsumerGroups = 256;     // persistent work-groups per consumer kind (one per CU)
@@ -1078,6 +1078,9 @@ template <int P, typename Copy>
 __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, float scale,
                                            __amdgpu_buffer_rsrc_t orc, uint32_t ocol, Copy&& copy_next) {
   const int l16 = lane & 15, lg = lane >> 4;
+  // the copies go first: they then have the whole chunk to land, and Y^T runs
+  // while the chain wave is in its VALU-heavy R / Delta phase instead of X
+  copy_next();
   const int rsw = kq_swz(l16);
   bf16x8 sb[4];
 #pragma unroll
@@ -1091,7 +1094,6 @@ __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, floa
       YT[m] = mfma16(sb[d], *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]),
                      YT[m]);
   }
-  copy_next();     // next chunk's operands, in flight until B3
   lds_barrier();   // B2
   bf16x8 dob[2];
 #pragma unroll
