@@ -213,19 +213,19 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
 // ============================================================================
 // prepass: chunk-local WY terms for one (record, v-head)
 // ============================================================================
-constexpr int kPrepassThreads = 256;
+constexpr int kPrepassThreads = 512;   // 8 waves: waves 0-3 serve v-head 2hq, waves 4-7 v-head 2hq+1
 constexpr int kMRow = 68;     // floats per LDS row of the 64x64 fp32 matrices (16-byte aligned)
 
-// 50 KB: three work-groups per CU.  T reuses the K / Q rows' space once the
-// grams have been formed.
+// 70.6 KB: two work-groups (four v-heads' worth) per CU.  The T matrices reuse
+// the K / Q rows' space once the grams have been formed.
 struct __align__(16) PrepassSmem {
   union {
     uint16_t kq[2][kChunk][kDim];   // K, Q rows (bf16, chunk-swizzled)
-    float tm[kChunk][kMRow];        // T = (I + N)^{-1}
+    float tm[kGva][kChunk][kMRow];  // T = (I + N)^{-1} per v-head of the pair
   } u;
-  float nm[kChunk][kMRow];          // N = strict lower beta_t rho K K^T; upper blocks are scratch
-  float lgam[kChunk];               // Gam_t / ln 2 (log2 cumulative decay)
-  float beta[kChunk];
+  float nm[kGva][kChunk][kMRow];    // N = strict lower beta_t rho K K^T; upper blocks are scratch
+  float lgam[kGva][kChunk];         // Gam_t / ln 2 (log2 cumulative decay)
+  float beta[kGva][kChunk];
 };
 
 // j-th lower 16x16 tile (mi >= ni) of a 4x4 tile grid, row by row:
@@ -252,75 +252,61 @@ __device__ __forceinline__ void block_store(float* Z, const f32x4& v, float sc, 
 // Record r of a batch of at most kFusedPlanSeqs sequences (one per thread),
 // found by the work-group itself (no plan launch): exclusive scan of
 // per-sequence chunk counts; the thread owning the sequence that contains r
-// publishes it.  The
-// work-group of record 0, v-head 0 also writes rec_start and the long / short
-// sequence lists for the consumer, as plan_kernel does.  Returns false when
-// record r does not exist.
-constexpr int kFusedPlanSeqs = 256;   // larger batches: the scan per work-group costs more than a launch
+// publishes it.  The work-group of record 0 also writes rec_start and the
+// long / short sequence lists for the consumer, as plan_kernel does.  Returns
+// false when record r does not exist.
+constexpr int kFusedPlanSeqs = kPrepassThreads;   // larger batches: a plan launch is cheaper
 
 __device__ bool find_record(int r, bool bookkeeping, const void* __restrict__ cu, int is64, int num_seqs,
                             long long T, int R, int* __restrict__ rec_start, int* __restrict__ lists,
                             int* scratch, long long& t0_out, int& c_out) {
+  // num_seqs <= kPrepassThreads: thread s owns sequence s (one read of its bounds)
   const int tid = threadIdx.x;
-  const int per = (num_seqs + kPrepassThreads - 1) / kPrepassThreads;
-  const int s_begin = tid * per;
-  const int s_end = min(num_seqs, s_begin + per);
-  int local = 0, nlong = 0;
-  for (int s = s_begin; s < s_end; ++s) {
-    long long t0, t1;
-    seq_bounds(cu, is64, s, T, t0, t1);
-    const long long nch = (t1 - t0 + kChunk - 1) / kChunk;
-    local += static_cast<int>(nch);
-    nlong += nch >= kLongChunks ? 1 : 0;
-  }
+  constexpr int kWaves = kPrepassThreads / 64;
+  long long t0 = 0, t1 = 0;
+  if (tid < num_seqs) seq_bounds(cu, is64, tid, T, t0, t1);
+  const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+  const int is_long = nch >= kLongChunks ? 1 : 0;
   if (tid == 0) scratch[0] = -1;
-  const int inc = block_scan<kPrepassThreads>(local, scratch + 8);
-  int base = inc - local;
-  int total = 0;
-  for (int j = 0; j < kPrepassThreads / 64; ++j) total += scratch[8 + j];
-  int lpos = 0, spos = 0;
+  const int inc = block_scan<kPrepassThreads>(nch, scratch + 16);
+  const int base = inc - nch;
+  if (nch > 0 && r >= base && r < base + nch) {
+    const long long c0 = t0 + static_cast<long long>(r - base) * kChunk;
+    scratch[0] = static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0));
+    scratch[2] = static_cast<int>(c0 & 0xffffffffLL);
+    scratch[3] = static_cast<int>(c0 >> 32);
+  }
   if (bookkeeping) {
-    const int nshort = max(s_end - s_begin, 0) - nlong;
-    const int inc_l = block_scan<kPrepassThreads>(nlong, scratch + 16);
-    const int inc_s = block_scan<kPrepassThreads>(nshort, scratch + 24);
-    lpos = inc_l - nlong;
-    spos = inc_s - nshort;
+    const int in_batch = tid < num_seqs ? 1 : 0;
+    const int inc_l = block_scan<kPrepassThreads>(is_long & in_batch, scratch + 32);
+    const int inc_s = block_scan<kPrepassThreads>((1 - is_long) & in_batch, scratch + 48);
+    if (tid < num_seqs) {
+      rec_start[tid] = base;
+      if (is_long) lists[2 + inc_l - 1] = tid;
+      else lists[2 + num_seqs + inc_s - 1] = tid;
+    }
     if (tid == 0) {
-      int tl = 0, ts = 0;
-      for (int j = 0; j < kPrepassThreads / 64; ++j) {
-        tl += scratch[16 + j];
-        ts += scratch[24 + j];
+      int tc = 0, tl = 0, ts = 0;
+      for (int j = 0; j < kWaves; ++j) {
+        tc += scratch[16 + j];
+        tl += scratch[32 + j];
+        ts += scratch[48 + j];
       }
       lists[0] = tl;
       lists[1] = ts;
-      rec_start[num_seqs] = min(total, R);
+      rec_start[num_seqs] = min(tc, R);
     }
-  }
-  for (int s = s_begin; s < s_end; ++s) {
-    long long t0, t1;
-    seq_bounds(cu, is64, s, T, t0, t1);
-    const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
-    if (r >= base && r < base + nch) {
-      scratch[0] = s;
-      scratch[1] = r - base;
-    }
-    if (bookkeeping) {
-      rec_start[s] = base;
-      if (nch >= kLongChunks) lists[2 + lpos++] = s;
-      else lists[2 + num_seqs + spos++] = s;
-    }
-    base += nch;
   }
   __syncthreads();
-  const int s = scratch[0];
-  if (s < 0) return false;
-  long long t0, t1;
-  seq_bounds(cu, is64, s, T, t0, t1);
-  t0_out = t0 + static_cast<long long>(scratch[1]) * kChunk;
-  c_out = static_cast<int>(min(static_cast<long long>(kChunk), t1 - t0_out));
+  c_out = scratch[0];
+  if (c_out < 0) return false;
+  t0_out = static_cast<long long>(static_cast<unsigned>(scratch[2])) | (static_cast<long long>(scratch[3]) << 32);
   return true;
 }
 
+// One work-group per (record, q/k head): the K / Q rows and both grams are
+// shared by the two v-heads of the GVA pair; gates, weighting, inverse and
+// packing run per v-head on waves 0-3 / 4-7.
 __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
@@ -329,16 +315,14 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
     uint16_t* __restrict__ ws_frag, float* __restrict__ ws_gam) {
   __shared__ PrepassSmem sm;
-  // linear id = r * 8 + h: v-head h runs on XCD h, as its consumer does
-  const int r = blockIdx.x / kVHeads;
-  const int h = blockIdx.x % kVHeads;
-  const int hq = h / kGva;
+  const int r = blockIdx.x / kQKHeads;
+  const int hq = blockIdx.x % kQKHeads;
   int c;
   long long t0;
   if (fused_plan) {
     // N's space is free until the grams; it holds the record search scratch
     if (!find_record(r, blockIdx.x == 0, cu, is64, num_seqs, T, R, rec_start, lists,
-                     reinterpret_cast<int*>(&sm.nm[0][0]), t0, c))
+                     reinterpret_cast<int*>(&sm.nm[0][0][0]), t0, c))
       return;
     __syncthreads();   // scratch read by every thread before N is written
   } else {
@@ -349,13 +333,16 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
   }
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = w >> 2;                 // which v-head of the pair this wave serves
+  const int wl = w & 3;                  // wave index within that v-head's group
+  const int h = kGva * hq + hh;
   const int lane = tid & 63;
   const int l16 = lane & 15;
   const int lg = lane >> 4;
 
-  // gate inputs first (wave 0, lane = token): their latency overlaps the row copies
+  // gate inputs first (waves 0 and 4, lane = token): their latency overlaps the row copies
   float a_t = 0.0f, b_t = 0.0f, alog = 0.0f, dtb = 0.0f;
-  if (w == 0) {
+  if (wl == 0) {
     const size_t gi = (t0 + min(lane, c - 1)) * kVHeads + h;
     a_t = bf2f(a[gi]);
     b_t = bf2f(b[gi]);
@@ -370,18 +357,18 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     const size_t qk0 = (static_cast<size_t>(t0) * kQKHeads + hq) * kDim;
     const char* kb = reinterpret_cast<const char*>(k + qk0);
     const char* qb = reinterpret_cast<const char*>(q + qk0);
-    const int row0 = 4 * w + (lane >> 4);          // + 16 j keeps row & 15
+    const int row0 = 4 * w + (lane >> 4);          // + 32 j keeps row & 15
     const uint32_t col = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(row0));
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t off = static_cast<uint32_t>(min(row0 + 16 * j, c - 1)) * (kQKHeads * kDim * 2) + col;
-      dma16(kb + off, &sm.u.kq[0][16 * j + 4 * w][0]);
-      dma16(qb + off, &sm.u.kq[1][16 * j + 4 * w][0]);
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t off = static_cast<uint32_t>(min(row0 + 32 * j, c - 1)) * (kQKHeads * kDim * 2) + col;
+      dma16(kb + off, &sm.u.kq[0][32 * j + 4 * w][0]);
+      dma16(qb + off, &sm.u.kq[1][32 * j + 4 * w][0]);
     }
   }
 
-  // ---- gates (wave 0, lane = token): Gam_t inclusive scan of log2 g, beta ----
-  if (w == 0) {
+  // ---- gates (waves 0 and 4, lane = token): Gam_t inclusive scan of log2 g, beta ----
+  if (wl == 0) {
     const int t = lane;
     // clamp: g = e^-100 is already 0 to fp32 working precision, and a finite
     // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
@@ -393,8 +380,8 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
       const float o = __shfl_up(scan, off, 64);
       if (lane >= off) scan += o;
     }
-    sm.lgam[t] = scan;
-    sm.beta[t] = bet;
+    sm.lgam[hh][t] = scan;
+    sm.beta[hh][t] = bet;
     const float last = __shfl(scan, c - 1, 64);
     float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * 2 * kChunk;
     gp[t] = t < c ? fast_exp2(scan) : 0.0f;
@@ -402,19 +389,21 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
   }
   __syncthreads();
 
-  // ---- grams on MFMA: N (K K^T, to LDS) and Aqk (Q K^T, to the workspace) ----
-  // Q K^T is formed transposed (A = K rows, B = Q rows): lane (lg, l16) then
-  // holds Aqk[16 mi + l16][16 ni + 4 lg + rr], which is exactly half (slots
-  // 4 (ni & 1) .. +3) of fragment (mi, ni >> 1) in permuted fragment order.
-  uint16_t* frag = ws_frag + (static_cast<size_t>(r) * kVHeads + h) * kFrags * kFragElems;
-  const int rsw = kq_swz(l16);
-  // wave w forms lower tiles j = w, w + 4, w + 8 (< 10) of both grams; all
-  // twelve accumulator chains are independent, so their MFMAs interleave
-  f32x4 akk[3], aqk[3];
+  // ---- grams on MFMA, shared by both v-heads: N (K K^T, to LDS) and Aqk
+  // (Q K^T, to the workspace).  Q K^T is formed transposed (A = K rows, B = Q
+  // rows): lane (lg, l16) then holds Aqk[16 mi + l16][16 ni + 4 lg + rr], which
+  // is exactly half (slots 4 (ni & 1) .. +3) of fragment (mi, ni >> 1) in
+  // permuted fragment order.  Wave w forms lower tiles w and w + 8 (< 10). ----
+  uint16_t* frag2[kGva];
 #pragma unroll
-  for (int n = 0; n < 3; ++n) {
+  for (int e = 0; e < kGva; ++e)
+    frag2[e] = ws_frag + (static_cast<size_t>(r) * kVHeads + kGva * hq + e) * kFrags * kFragElems;
+  const int rsw = kq_swz(l16);
+  f32x4 akk[2], aqk[2];
+#pragma unroll
+  for (int n = 0; n < 2; ++n) {
     int mi, ni;
-    lower_tile(min(w + 4 * n, 9), mi, ni);
+    lower_tile(min(w + 8 * n, 9), mi, ni);
     akk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
     aqk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -428,62 +417,67 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     }
   }
 #pragma unroll
-  for (int n = 0; n < 3; ++n) {
-    if (w + 4 * n >= 10) break;   // wave-uniform
+  for (int n = 0; n < 2; ++n) {
+    if (w + 8 * n >= 10) break;   // wave-uniform
     int mi, ni;
-    lower_tile(w + 4 * n, mi, ni);
-    {
-      // akk[n][rr] = K_t . K_i, t = 16 mi + 4 lg + rr, i = 16 ni + l16
-      const int i = 16 * ni + l16;
-      const float gi_ = sm.lgam[i];
-      const f32x4 gt = *reinterpret_cast<const f32x4*>(&sm.lgam[16 * mi + 4 * lg]);
-      const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[16 * mi + 4 * lg]);
+    lower_tile(w + 8 * n, mi, ni);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int t = 16 * mi + 4 * lg + rr;
-        sm.nm[t][i] = i < t ? bt[rr] * fast_exp2(gt[rr] - gi_) * akk[n][rr] : 0.0f;
-      }
-    }
-    {
-      // aqk[n][rr] = K_i . Q_t (transposed), i = 16 ni + 4 lg + rr, t = 16 mi + l16
-      const int t = 16 * mi + l16;
-      const float gt = sm.lgam[t];
-      const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&sm.lgam[16 * ni + 4 * lg]);
-      float x[4];
+    for (int e = 0; e < kGva; ++e) {
+      {
+        // akk[n][rr] = K_t . K_i, t = 16 mi + 4 lg + rr, i = 16 ni + l16
+        const int i = 16 * ni + l16;
+        const float gi_ = sm.lgam[e][i];
+        const f32x4 gt = *reinterpret_cast<const f32x4*>(&sm.lgam[e][16 * mi + 4 * lg]);
+        const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[e][16 * mi + 4 * lg]);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = 16 * ni + 4 * lg + rr;
-        x[rr] = i <= t ? fast_exp2(gt - gi4[rr]) * aqk[n][rr] : 0.0f;
+        for (int rr = 0; rr < 4; ++rr) {
+          const int t = 16 * mi + 4 * lg + rr;
+          sm.nm[e][t][i] = i < t ? bt[rr] * fast_exp2(gt[rr] - gi_) * akk[n][rr] : 0.0f;
+        }
       }
-      *reinterpret_cast<u32x2*>(frag + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + lane) * 8 + 4 * (ni & 1)) =
-          u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
+      {
+        // aqk[n][rr] = K_i . Q_t (transposed), i = 16 ni + 4 lg + rr, t = 16 mi + l16
+        const int t = 16 * mi + l16;
+        const float gt = sm.lgam[e][t];
+        const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&sm.lgam[e][16 * ni + 4 * lg]);
+        float x[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * ni + 4 * lg + rr;
+          x[rr] = i <= t ? fast_exp2(gt - gi4[rr]) * aqk[n][rr] : 0.0f;
+        }
+        *reinterpret_cast<u32x2*>(frag2[e] + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + lane) * 8 + 4 * (ni & 1)) =
+            u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
+      }
     }
   }
-  // the six half-fragments of Aqk above the diagonal: (mi, ni) = (0,1) (0,2)
-  // (0,3) (1,2) (1,3) (2,3)
-  for (int z = tid; z < 6 * 64; z += kPrepassThreads) {
-    const int zj = z >> 6, zl = z & 63;
+  // the six half-fragments of Aqk above the diagonal, both v-heads: (mi, ni) =
+  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
+  for (int z = tid; z < kGva * 6 * 64; z += kPrepassThreads) {
+    const int e = z / (6 * 64), zj = (z >> 6) % 6, zl = z & 63;
     const int mi = zj < 3 ? 0 : (zj < 5 ? 1 : 2);
     const int ni = zj < 3 ? zj + 1 : (zj < 5 ? zj - 1 : 3);
-    *reinterpret_cast<u32x2*>(frag + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + zl) * 8 + 4 * (ni & 1)) =
+    *reinterpret_cast<u32x2*>(frag2[e] + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + zl) * 8 + 4 * (ni & 1)) =
         u32x2{0u, 0u};
   }
   __syncthreads();   // N complete; K / Q space becomes T
 
-  // ---- T = (I + N)^{-1}: diagonal 16x16 blocks by forward substitution ----
+  // ---- T = (I + N)^{-1} per v-head: diagonal 16x16 blocks by forward substitution ----
+  float (*nmh)[kMRow] = sm.nm[hh];
+  float (*tmh)[kMRow] = sm.u.tm[hh];
   if (lane < 16) {
-    const int base = 16 * w;
+    const int base = 16 * wl;
     const int j = lane;
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       float acc = (i == j) ? 1.0f : 0.0f;
 #pragma unroll
-      for (int m2 = 0; m2 < i; ++m2) acc = fmaf(-sm.nm[base + i][base + m2], x[m2], acc);
+      for (int m2 = 0; m2 < i; ++m2) acc = fmaf(-nmh[base + i][base + m2], x[m2], acc);
       x[i] = acc;
     }
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sm.u.tm[base + i][base + j] = x[i];
+    for (int i = 0; i < 16; ++i) tmh[base + i][base + j] = x[i];
   }
 
   // ---- off-diagonal blocks by distance on fp32 MFMA:
@@ -491,38 +485,44 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
 #pragma unroll
   for (int dist = 1; dist < 4; ++dist) {
     __syncthreads();
-    if (w < 4 - dist) {
-      const int bj = w, bi = w + dist;
-      f32x4 p = {0.f, 0.f, 0.f, 0.f};
+    if (wl < 4 - dist) {
+      const int bj = wl, bi = wl + dist;
+      // one accumulator per block product (independent MFMA chains), summed after
+      f32x4 pu[3];
 #pragma unroll
       for (int u = 0; u < dist; ++u)
-        p = block_prod(p, &sm.nm[16 * bi][16 * (bj + u)], &sm.u.tm[16 * (bj + u)][16 * bj], l16, lg);
-      float* scr = &sm.nm[16 * bj][16 * bi];
-      block_store(scr, p, 1.0f, l16, lg);
+        pu[u] = block_prod(f32x4{0.f, 0.f, 0.f, 0.f}, &nmh[16 * bi][16 * (bj + u)], &tmh[16 * (bj + u)][16 * bj],
+                           l16, lg);
+      f32x4 pacc = pu[0];
+#pragma unroll
+      for (int u = 1; u < dist; ++u) pacc += pu[u];
+      float* scr = &nmh[16 * bj][16 * bi];
+      block_store(scr, pacc, 1.0f, l16, lg);
       f32x4 tv = {0.f, 0.f, 0.f, 0.f};
-      tv = block_prod(tv, &sm.u.tm[16 * bi][16 * bi], scr, l16, lg);
-      block_store(&sm.u.tm[16 * bi][16 * bj], tv, -1.0f, l16, lg);
+      tv = block_prod(tv, &tmh[16 * bi][16 * bi], scr, l16, lg);
+      block_store(&tmh[16 * bi][16 * bj], tv, -1.0f, l16, lg);
     }
   }
   __syncthreads();
 
-  // ---- pack Tb = T diag(beta) as fp16 (permuted fragment order) ----
+  // ---- pack Tb = T diag(beta) as fp16 (permuted fragment order), per v-head ----
   // fragment (m, d), lane l: row t = 16 m + l % 16, slots s: i = perm_depth(d, l / 16, s)
-  for (int qi = tid; qi < 512; qi += kPrepassThreads) {
+  for (int qi = tid & 255; qi < 512; qi += 256) {
     const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
     const int t = 16 * m + (l & 15);
     const int i0 = 32 * d + 4 * (l >> 4);
-    const f32x4 ta = *reinterpret_cast<const f32x4*>(&sm.u.tm[t][i0]);
-    const f32x4 tb = *reinterpret_cast<const f32x4*>(&sm.u.tm[t][i0 + 16]);
-    const f32x4 ba = *reinterpret_cast<const f32x4*>(&sm.beta[i0]);
-    const f32x4 bb = *reinterpret_cast<const f32x4*>(&sm.beta[i0 + 16]);
+    const int e = tid >> 8;
+    const f32x4 ta = *reinterpret_cast<const f32x4*>(&sm.u.tm[e][t][i0]);
+    const f32x4 tb = *reinterpret_cast<const f32x4*>(&sm.u.tm[e][t][i0 + 16]);
+    const f32x4 ba = *reinterpret_cast<const f32x4*>(&sm.beta[e][i0]);
+    const f32x4 bb = *reinterpret_cast<const f32x4*>(&sm.beta[e][i0 + 16]);
     float x[8];
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       x[s] = i0 + s <= t ? ta[s] * ba[s] : 0.0f;
       x[4 + s] = i0 + 16 + s <= t ? tb[s] * bb[s] : 0.0f;
     }
-    *reinterpret_cast<u32x4*>(frag + qi * 8) =
+    *reinterpret_cast<u32x4*>(frag2[e] + qi * 8) =
         u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
   }
 }
@@ -1292,7 +1292,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                         total_tokens, static_cast<int>(R), rec_start,
                                                         recs, lists);
-  prepass_kernel<<<dim3(static_cast<unsigned>(R * kVHeads)), dim3(kPrepassThreads), 0, st>>>(
+  prepass_kernel<<<dim3(static_cast<unsigned>(R * kQKHeads)), dim3(kPrepassThreads), 0, st>>>(
       qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
       static_cast<int>(R), fused_plan, rec_start, lists, frag, gam);
   // persistent grids: one work-group per CU per consumer kind at most
