@@ -13,19 +13,25 @@
 // cumulative decay), so C = 64 is safe where the reference's X-space form
 // (solution/triton/kernel.py:421-425) divides by G.
 //
-// Three launches, all on the caller's stream:
-//   plan     : 1 work-group; chunk records (seq, first token, length) for all
-//              sequences from cu_seqlens, with no host synchronisation.
-//   prepass  : one work-group per (record, v-head), all records in parallel:
-//              gates, K K^T / Q K^T on MFMA, fp32 blocked triangular inverse,
-//              and the packed MFMA operands Tb (fp16), Aqk (bf16) plus
+// Launches, all on the caller's stream, no host synchronisation:
+//   plan     : (batches of more than 512 sequences only) 1 work-group: chunk
+//              records, segment length and work lists from cu_seqlens.  For
+//              smaller batches work-group 0 of the prepass plans and the other
+//              prepass work-groups find their own records.
+//   prepass  : one work-group per (record, q/k head), all records in
+//              parallel: gates, K K^T / Q K^T on MFMA, fp32 blocked triangular
+//              inverse, and the packed MFMA operands Tb (fp16), Aqk (bf16) plus
 //              gam / tail, written to the workspace.
-//   consumer : one work-group per (seq, v-head); each of its 8 waves (two per
-//              SIMD) owns one 16-wide V tile and runs the whole chunk
-//              recurrence for it with the state in MFMA registers; the chunk
-//              operands (K, Q, V rows, packed Tb / Aqk, gates) are copied from
-//              global memory straight into double-buffered LDS and shared by
-//              the 8 waves.
+//   consumer : persistent work-groups.  Long sequences are cut into segments
+//              of L chunks (L chosen by the plan); every segment runs at once,
+//              segments >= 1 twice (zero initial state with the real V, and
+//              identity initial state with V = 0), each run split over two
+//              work-groups of 64 value rows whose chain waves carry the state
+//              in MFMA registers.  Short sequences run one work-group per
+//              (sequence, v-head).  Chunk operands are copied from global
+//              memory straight into double-buffered LDS.
+//   scan     : S_{j+1} = S_j M_j + B_j over the segments of each sequence.
+//   correct  : O = O0 + OI S_j^T for the tokens of segments >= 1.
 //
 // Precision policy (fp32 accumulation everywhere): K, Q, V are bf16 inputs, so
 // their products are exact.  S enters K S^T and Q S^T as a single bf16; Tb and
@@ -58,13 +64,78 @@ __host__ __device__ constexpr int perm_depth(int d, int lg, int s) {
   return 32 * d + 16 * (s >> 2) + 4 * lg + (s & 3);
 }
 
+// ---- segments ---------------------------------------------------------------
+// A long sequence is cut into segments of L chunks (L chosen per call by the
+// planner).  Segment 0 runs from the true initial state.  Segment j >= 1 runs
+// twice, concurrently with all others: the "B-run" from a zero state with the
+// real V (outputs O0, final state B_j) and the "M-run" from the identity with
+// V = 0 (outputs OI, final state M_j).  The recurrence is linear in (S, V), so
+//   S_{j+1} = S_j M_j + B_j,          O_j = O0_j + OI_j S_j^T,
+// which a short scan over segments and a parallel correction pass resolve.
+constexpr int kMinSegChunks = 4;   // shortest segment the planner may choose
+constexpr int kMaxSegChunks = 1024;   // longest finite candidate (segments of multi-segment sequences)
+constexpr int kMSlotElems = 8 * 4 * 2 * 64 * 8;   // M_j^T as bf16 hi / lo MFMA fragments, per head
+constexpr int kFSlotElems = 8 * 4 * 64 * 8;       // a state as bf16 correction fragments, per head
+
+// Upper bound on the segments of all multi-segment sequences: a sequence of
+// tau tokens split into n >= 2 segments of L >= kMinSegChunks chunks has
+// tau > 64 L and n = ceil(tau / 64 L) < 2 tau / 64 L, so n summed over
+// sequences stays below T / (32 kMinSegChunks).
+__host__ __device__ inline long long max_segments(long long tokens) {
+  return tokens / (32 * kMinSegChunks) + 1;
+}
+
+// lists: header, multi-segment entries, later-segment table, runs (two int4
+// each), short sequences.  Everything a kernel needs about one work item sits
+// in one entry, so an item costs one dependent load before its data.
+//   hdr[0] runs, [1] short sequences, [2] segment length L (chunks),
+//   [3] multi-segment sequences, [4] segments >= 1 over all sequences
+//   multi[e]   = (seq, first slot, segments, 0)
+//   segs[i]    = (first token lo, hi, tokens in the segment, slot holding the
+//                 state before the segment) for every segment >= 1
+//   runs[2i]   = (seq, flags | tokens of the run's last chunk << 8,
+//                 final-state slot or -1 for new_state, first record)
+//   runs[2i+1] = (first token lo, hi, chunks with records, chunks)
+//   flags: kRunM (M-run), kRunFromState (initial state from `state`)
+constexpr int kListHdr = 8;
+constexpr int kRunM = 1;
+constexpr int kRunFromState = 2;
+__host__ __device__ inline long long max_runs(int num_seqs, long long gcap) { return 2 * gcap + num_seqs; }
+
+struct ListView {
+  int* hdr;
+  int4* multi;
+  int4* segs;
+  int4* runs;
+  int* shorts;
+};
+
+__host__ __device__ inline ListView list_view(int* lists, int num_seqs, long long gcap) {
+  ListView v;
+  v.hdr = lists;
+  v.multi = reinterpret_cast<int4*>(lists + kListHdr);
+  v.segs = v.multi + num_seqs;
+  v.runs = v.segs + gcap;
+  v.shorts = reinterpret_cast<int*>(v.runs + 2 * max_runs(num_seqs, gcap));
+  return v;
+}
+
+__host__ __device__ inline size_t list_ints(int num_seqs, long long gcap) {
+  return kListHdr + 4 * static_cast<size_t>(num_seqs) + 4 * static_cast<size_t>(gcap) +
+         8 * static_cast<size_t>(max_runs(num_seqs, gcap)) + static_cast<size_t>(num_seqs);
+}
+
 // ---- workspace layout -------------------------------------------------------
 struct WsLayout {
   size_t frag_off;     // u16  [R][8][2][4096]   (Tb fp16, Aqk bf16)
   size_t gam_off;      // f32  [R][8][2][64]     (gam, tail)
   size_t start_off;    // i32  [N + 1]           record start per sequence
-  size_t list_off;     // i32  [2 + 2N]          counts (long, short), long list, short list
+  size_t list_off;     // i32  lists (see list_view)
   size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
+  size_t slotb_off;    // f32  [G][8][128][128]  B_j, then (after the scan) the state after segment j
+  size_t slotm_off;    // u16  [G][8][kMSlotElems] M_j^T fragments
+  size_t slotf_off;    // u16  [G][8][kFSlotElems] state before segment j as correction fragments
+  size_t oi_off;       // u16  [T][8][128]       M-run outputs OI (rows of segments >= 1)
   size_t total;
 };
 
@@ -77,12 +148,18 @@ __host__ __device__ inline long long max_records(int num_seqs, long long tokens)
 __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   WsLayout L;
   const size_t R = static_cast<size_t>(max_records(num_seqs, tokens));
+  const size_t G = static_cast<size_t>(max_segments(tokens));
+  const size_t N = static_cast<size_t>(num_seqs);
   size_t off = 0;
   L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kFragElems * sizeof(uint16_t));
   L.gam_off = off;   off = align256(off + R * kVHeads * 2 * kChunk * sizeof(float));
-  L.start_off = off; off = align256(off + (static_cast<size_t>(num_seqs) + 1) * sizeof(int));
-  L.list_off = off;  off = align256(off + (2 + 2 * static_cast<size_t>(num_seqs)) * sizeof(int));
+  L.start_off = off; off = align256(off + (N + 1) * sizeof(int));
+  L.list_off = off;  off = align256(off + list_ints(num_seqs, static_cast<long long>(G)) * sizeof(int));
   L.rec_off = off;   off = align256(off + R * sizeof(int4));
+  L.slotb_off = off; off = align256(off + G * kVHeads * kHeadState * sizeof(float));
+  L.slotm_off = off; off = align256(off + G * kVHeads * kMSlotElems * sizeof(uint16_t));
+  L.slotf_off = off; off = align256(off + G * kVHeads * kFSlotElems * sizeof(uint16_t));
+  L.oi_off = off;    off = align256(off + static_cast<size_t>(tokens) * kVHeads * kDim * sizeof(uint16_t));
   L.total = off;
   return L;
 }
@@ -105,24 +182,53 @@ __device__ __forceinline__ void seq_bounds(const void* cu, int is64, int s, long
 }
 
 // ============================================================================
-// plan: record numbering (exclusive scan of per-sequence chunk counts)
+// plan: record numbering, segment length, consumer work lists
 // ============================================================================
 constexpr int kPlanThreads = 1024;
+constexpr int kConsumerGroups = 256;     // persistent work-groups per consumer kind (one per CU)
 
 // Sequences of at least this many chunks run on the split consumer (chunk
 // time bounds the call); shorter ones on the full-head consumer (throughput).
 constexpr int kLongChunks = 2;
 
-// Inclusive prefix sum over the NT threads of the work-group: shuffle scan
-// inside each wave, then one pass over the wave totals (wave_tot: NT / 64 ints).
+// ---- wave / work-group reductions on DPP (no LDS traffic inside a wave) ----
+// update_dpp with old = 0 and bound_ctrl off: lanes whose source lies outside
+// their row (or rows masked off) read 0.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ int dpp0(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, ROWS, 0xf, false);
+}
+
+// Inclusive prefix sum over the 64 lanes: row_shr 1, 2, 4, 8 within rows of
+// 16, then row_bcast 15 / 31 carry the row totals into the rows above.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += dpp0<0x111>(x);
+  x += dpp0<0x112>(x);
+  x += dpp0<0x114>(x);
+  x += dpp0<0x118>(x);
+  x += dpp0<0x142, 0xa>(x);
+  x += dpp0<0x143, 0xc>(x);
+  return x;
+}
+
+__device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_incl_sum(x), 63); }
+
+// Maximum over the lanes of non-negative values (0 is the identity).
+__device__ __forceinline__ int wave_max0(int x) {
+  x = max(x, dpp0<0x111>(x));
+  x = max(x, dpp0<0x112>(x));
+  x = max(x, dpp0<0x114>(x));
+  x = max(x, dpp0<0x118>(x));
+  x = max(x, dpp0<0x142, 0xa>(x));
+  x = max(x, dpp0<0x143, 0xc>(x));
+  return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Inclusive prefix sum over the NT threads of the work-group (wave_tot: NT / 64 ints).
 template <int NT>
 __device__ __forceinline__ int block_scan(int x, int* wave_tot) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int o = __shfl_up(x, off, 64);
-    if (lane >= off) x += o;
-  }
+  x = wave_incl_sum(x);
   if (lane == 63) wave_tot[wv] = x;
   __syncthreads();
   int add = 0;
@@ -131,47 +237,320 @@ __device__ __forceinline__ int block_scan(int x, int* wave_tot) {
   return x + add;
 }
 
+// K prefix sums at once: x becomes the inclusive scan, total the block sums
+// (wave_tot: NT / 64 * K ints).
+template <int NT, int K>
+__device__ __forceinline__ void block_scan_v(int (&x)[K], int* wave_tot, int (&total)[K]) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < K; ++i) x[i] = wave_incl_sum(x[i]);
+  if (lane == 63) {
+#pragma unroll
+    for (int i = 0; i < K; ++i) wave_tot[wv * K + i] = x[i];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    int add = 0, tot = 0;
+    for (int j = 0; j < NT / 64; ++j) {
+      const int t = wave_tot[j * K + i];
+      add += j < wv ? t : 0;
+      tot += t;
+    }
+    x[i] += add;
+    total[i] = tot;
+  }
+  __syncthreads();
+}
+
+// Candidate segment lengths (chunks): 4, 6, ..., 32, then 40, 48, 64, 80,
+// 96, 128, ... (5, 6, 8 x 2^k) up to 1024, and "no split".
+constexpr int kSegCands = 31;
+__device__ __forceinline__ int seg_cand(int i) {
+  if (i >= kSegCands - 1) return 1 << 30;
+  if (i < 15) return 4 + 2 * i;
+  const int j = i - 15, m = j % 3;
+  return (m == 0 ? 5 : (m == 1 ? 6 : 8)) << (3 + j / 3);
+}
+
+// Partial runs are ordered by length, longest first: exact below 64 chunks,
+// by power of two above.
+constexpr int kBuckets = 96;
+__device__ __forceinline__ int len_bucket(int len) { return len < 64 ? len : 64 + (31 - __clz(len)); }
+
+// Runs of one sequence for segment length L.  Segments 0 .. nseg-2 have L
+// chunks, the last one `last` (1 .. L).  Full-length runs: segment 0's, and
+// the B- and M-run of every other full segment; a shorter last segment gives
+// one or two "partial" runs.
+struct SeqPlan {
+  int is_long, nseg, multi, full_seg, full_runs, part_runs, last;
+};
+
+__device__ __forceinline__ SeqPlan seq_plan(int nch, int L) {
+  SeqPlan p = {0, 0, 0, 0, 0, 0, 0};
+  if (nch < kLongChunks) return p;
+  p.is_long = 1;
+  p.nseg = (nch - 1) / L + 1;
+  p.multi = p.nseg >= 2 ? 1 : 0;
+  p.last = nch - (p.nseg - 1) * L;
+  p.full_seg = p.last == L ? p.nseg : p.nseg - 1;
+  p.full_runs = p.full_seg > 0 ? 2 * p.full_seg - 1 : 0;
+  p.part_runs = p.last == L ? 0 : (p.nseg == 1 ? 1 : 2);
+  return p;
+}
+
+// Scratch ints used by plan_batch.
+constexpr int kPsVals = 3 * kSegCands + 2;
+constexpr int kPsCand = 0;                                   // [waves][kPsVals]
+constexpr int kPsScan = kPsCand + (kPlanThreads / 64) * kPsVals;   // [waves][5]
+constexpr int kPsHist = kPsScan + (kPlanThreads / 64) * 5;
+constexpr int kPsCur = kPsHist + kBuckets;
+constexpr int kPsMisc = kPsCur + kBuckets;
+constexpr int kPlanScratch = kPsMisc + 4;
+
+// Plans the call for the whole batch with one work-group of NT threads, thread
+// i owning a contiguous range of sequences: rec_start (chunk record of each
+// sequence's first chunk), the segment length, and the work lists of the
+// split consumer (runs, longest first), the full-head consumer (short
+// sequences), the scan (multi-segment sequences) and the correction (segments
+// >= 1).
+//
+// Segment length: for each candidate L the split consumer's critical path is
+// about max(L + o, (16 W(L) + 16 o runs(L)) / groups) chunk steps, W(L) = sum
+// over long sequences of (2 nch - min(nch, L)) chunk runs per (value half,
+// v-head), o the per-item overhead; the scan adds about half a chunk step per
+// segment and segmenting at all about 1.5 steps.  Candidates whose segments
+// would not fit the workspace slots are skipped.
+// Returns the thread's first record index.  t0_first / t1_first: bounds of the
+// thread's first sequence when the caller already read them (t1_first < 0:
+// not known).
+template <int NT>
+__device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, long long T, int R, int gcap,
+                          int* __restrict__ rec_start, int* __restrict__ lists, int* ps, int& total_recs,
+                          long long t0_first = 0, long long t1_first = -1) {
+  constexpr int kW = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int per = (num_seqs + NT - 1) / NT;
+  const int s_begin = min(tid * per, num_seqs);
+  const int s_end = min(num_seqs, s_begin + per);
+  long long b0 = 0, b1 = 0;   // bounds of the first sequence, read once
+  if (s_begin < s_end) {
+    if (t1_first >= 0) {
+      b0 = t0_first;
+      b1 = t1_first;
+    } else {
+      seq_bounds(cu, is64, s_begin, T, b0, b1);
+    }
+  }
+  auto bounds = [&](int s, long long& t0, long long& t1) {
+    if (s == s_begin) {
+      t0 = b0;
+      t1 = b1;
+    } else {
+      seq_bounds(cu, is64, s, T, t0, t1);
+    }
+  };
+  auto chunks = [&](int s) {
+    long long t0, t1;
+    bounds(s, t0, t1);
+    return static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+  };
+
+  // ---- pass 1: statistics per candidate segment length ----
+  // A: sum of min(nch, L); B: slots (segments of multi-segment sequences);
+  // C: runs (2 nseg - 1 per long sequence)
+  int A[kSegCands], B[kSegCands], C[kSegCands];
+#pragma unroll
+  for (int i = 0; i < kSegCands; ++i) A[i] = B[i] = C[i] = 0;
+  int suml = 0, maxl = 0;
+  for (int s = s_begin; s < s_end; ++s) {
+    const int nch = chunks(s);
+    if (nch < kLongChunks) continue;
+    suml += nch;
+    maxl = max(maxl, nch);
+#pragma unroll
+    for (int i = 0; i < kSegCands; ++i) {
+      const int Lc = seg_cand(i);
+      const int nseg = (nch - 1) / Lc + 1;
+      A[i] += min(nch, Lc);
+      B[i] += nseg > 1 ? nseg : 0;
+      C[i] += 2 * nseg - 1;
+    }
+  }
+  // waves without long sequences (most of a short-sequence batch) skip the reductions
+  if (__builtin_amdgcn_ballot_w64(maxl > 0) != 0) {
+#pragma unroll
+    for (int i = 0; i < kSegCands; ++i) {
+      A[i] = wave_sum(A[i]);
+      B[i] = wave_sum(B[i]);
+      C[i] = wave_sum(C[i]);
+    }
+    suml = wave_sum(suml);
+    maxl = wave_max0(maxl);
+  }
+  if (lane == 0) {
+    int* pw = ps + kPsCand + wv * kPsVals;
+#pragma unroll
+    for (int i = 0; i < kSegCands; ++i) {
+      pw[i] = A[i];
+      pw[kSegCands + i] = B[i];
+      pw[2 * kSegCands + i] = C[i];
+    }
+    pw[3 * kSegCands] = suml;
+    pw[3 * kSegCands + 1] = maxl;
+  }
+  for (int i = tid; i < 2 * kBuckets; i += NT) ps[kPsHist + i] = 0;
+  __syncthreads();
+  if (wv == 0) {
+    // lane i < kSegCands evaluates candidate i, in chunk steps of the split
+    // consumer: the longest run and the average work-group load (chunk runs
+    // plus a per-item overhead) bound the critical path; the scan adds half a
+    // step per segment and segmenting at all 1.5 steps.  The minimum over the
+    // lanes wins, ties to the longer segments.
+    float sl = 0.f, a = 0.f, runs = 0.f;
+    long long slots = 0;
+    int ml = 0;
+    const int ci = min(lane, kSegCands - 1);
+    for (int j = 0; j < kW; ++j) {
+      const int* pj = ps + kPsCand + j * kPsVals;
+      sl += static_cast<float>(pj[3 * kSegCands]);
+      ml = max(ml, pj[3 * kSegCands + 1]);
+      a += static_cast<float>(pj[ci]);
+      slots += pj[kSegCands + ci];
+      runs += static_cast<float>(pj[2 * kSegCands + ci]);
+    }
+    constexpr float kItemOverhead = 1.0f;   // chunk steps per work item (metadata, state, first copies)
+    const int Lc = seg_cand(ci);
+    const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
+    const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
+    const int nseg_max = ml > 0 ? (ml - 1) / Lc + 1 : 0;
+    const float est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    // key: estimate in 1/16 steps, then the longer candidate; invalid lanes hold the maximum
+    const int q = static_cast<int>(fminf(est * 16.f, 1.0e7f));
+    const int key = (lane < kSegCands && slots <= gcap) ? q * 64 + (63 - lane) : 0x7fffffff;
+    // minimum over the lanes: the maximum of the complements
+    const int best = 0x7fffffff - wave_max0(0x7fffffff - key);
+    if (lane == 0) ps[kPsMisc] = seg_cand(63 - (best & 63));
+  }
+  __syncthreads();
+  const int L = ps[kPsMisc];
+
+  // ---- pass 2: per-sequence counts and their prefix sums ----
+  // v: records, short sequences, multi-segment sequences, slots, full runs
+  int v[5] = {0, 0, 0, 0, 0};
+  for (int s = s_begin; s < s_end; ++s) {
+    const int nch = chunks(s);
+    const SeqPlan p = seq_plan(nch, L);
+    v[0] += nch;
+    v[1] += p.is_long ? 0 : 1;
+    v[2] += p.multi;
+    v[3] += p.multi ? p.nseg : 0;
+    v[4] += p.full_runs;
+    if (p.part_runs) atomicAdd(&ps[kPsHist + len_bucket(p.last)], p.part_runs);
+  }
+  int own[5], tot[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) own[i] = v[i];
+  block_scan_v<NT, 5>(v, ps + kPsScan, tot);
+  total_recs = tot[0];
+  const ListView lv = list_view(lists, num_seqs, gcap);
+  if (wv == 0) {
+    // partial runs follow the full-length ones, longest first: descending
+    // exclusive prefix of the bucket counts, two buckets per lane
+    const int b0_ = kBuckets - 1 - 2 * lane, b1_ = b0_ - 1;
+    const int h0 = lane < kBuckets / 2 ? ps[kPsHist + b0_] : 0;
+    const int h1 = lane < kBuckets / 2 ? ps[kPsHist + b1_] : 0;
+    const int inc = wave_incl_sum(h0 + h1);
+    const int ex = tot[4] + inc - h0 - h1;
+    if (lane < kBuckets / 2) {
+      ps[kPsCur + b0_] = ex;
+      ps[kPsCur + b1_] = ex + h0;
+    }
+    if (lane == 63) {
+      lv.hdr[0] = tot[4] + inc;
+      lv.hdr[1] = tot[1];
+      lv.hdr[2] = L;
+      lv.hdr[3] = tot[2];
+      lv.hdr[4] = tot[3] - tot[2];
+      rec_start[num_seqs] = min(tot[0], R);
+    }
+  }
+  __syncthreads();
+
+  // ---- pass 3: emit ----
+  int rb = v[0] - own[0], sp = v[1] - own[1], mp = v[2] - own[2];
+  int gb = v[3] - own[3], fp = v[4] - own[4];
+  const int rb0 = rb;
+  for (int s = s_begin; s < s_end; ++s) {
+    long long t0, t1;
+    bounds(s, t0, t1);
+    const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+    const SeqPlan p = seq_plan(nch, L);
+    const int rec0 = rb;
+    rec_start[s] = rb;
+    rb += nch;
+    if (!p.is_long) {
+      lv.shorts[sp++] = s;
+      continue;
+    }
+    const int g0 = p.multi ? gb : 0;
+    if (p.multi) {
+      // later-segment table: entries gb - mp .. (one per segment >= 1)
+      lv.multi[mp] = make_int4(s, gb, p.nseg, 0);
+      for (int j = 1; j < p.nseg; ++j) {
+        const long long c0 = t0 + static_cast<long long>(j) * L * kChunk;
+        const int tok = static_cast<int>(min(t1 - c0, static_cast<long long>(L) * kChunk));
+        lv.segs[gb - mp + j - 1] =
+            make_int4(static_cast<int>(c0 & 0xffffffffLL), static_cast<int>(c0 >> 32), tok, gb + j - 1);
+      }
+      ++mp;
+      gb += p.nseg;
+    }
+    // one run of segment j (flags: kRunM / kRunFromState) at list position pos
+    auto emit_run = [&](int pos, int j, bool mrun) {
+      const long long i0 = static_cast<long long>(j) * L;
+      const int nrun = static_cast<int>(min(static_cast<long long>(nch) - i0, static_cast<long long>(L)));
+      const long long c0 = t0 + i0 * kChunk;
+      // tokens of the run's last chunk: 64 unless the run ends the sequence
+      const long long run_end = min(t1, c0 + static_cast<long long>(nrun) * kChunk);
+      const int last_tok = static_cast<int>(run_end - (c0 + static_cast<long long>(nrun - 1) * kChunk));
+      const long long rfirst = rec0 + i0;
+      // chunks whose records exist (overlapping cu_seqlens can exhaust the capacity)
+      const int nvalid = static_cast<int>(max(0LL, min(static_cast<long long>(nrun), R - rfirst)));
+      const int flags = (mrun ? kRunM : 0) | (!mrun && j == 0 ? kRunFromState : 0);
+      const int slot = p.multi ? g0 + j : -1;
+      lv.runs[2 * pos] = make_int4(s, flags | (last_tok << 8), slot, static_cast<int>(min(rfirst, 0x7fffffffLL)));
+      lv.runs[2 * pos + 1] = make_int4(static_cast<int>(c0 & 0xffffffffLL), static_cast<int>(c0 >> 32), nvalid, nrun);
+    };
+    for (int j = 0; j < p.full_seg; ++j) {
+      emit_run(fp++, j, false);
+      if (j > 0) emit_run(fp++, j, true);
+    }
+    if (p.part_runs) {
+      const int pos = atomicAdd(&ps[kPsCur + len_bucket(p.last)], p.part_runs);
+      const int j = p.nseg - 1;
+      emit_run(pos, j, false);
+      if (p.part_runs == 2) emit_run(pos + 1, j, true);
+    }
+  }
+  return rb0;
+}
+
+// Separate planning launch for large batches: plan_batch plus the flat record
+// table the prepass reads.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
-    const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
+    const void* __restrict__ cu, int is64, int num_seqs, long long T, int R, int gcap,
     int* __restrict__ rec_start, int4* __restrict__ recs, int* __restrict__ lists) {
-  __shared__ int wave_tot[3][kPlanThreads / 64];
+  __shared__ int ps[kPlanScratch];
   const int tid = threadIdx.x;
   const int per = (num_seqs + kPlanThreads - 1) / kPlanThreads;
-  const int s_begin = tid * per;
+  const int s_begin = min(tid * per, num_seqs);
   const int s_end = min(num_seqs, s_begin + per);
-  int local = 0, nlong = 0;
+  int total_recs;
+  int base = plan_batch<kPlanThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, ps, total_recs);
   for (int s = s_begin; s < s_end; ++s) {
     long long t0, t1;
     seq_bounds(cu, is64, s, T, t0, t1);
-    const long long nch = (t1 - t0 + kChunk - 1) / kChunk;
-    local += static_cast<int>(nch);
-    nlong += nch >= kLongChunks ? 1 : 0;
-  }
-  const int nshort = max(s_end - s_begin, 0) - nlong;
-  const int inc_c = block_scan<kPlanThreads>(local, wave_tot[0]);
-  const int inc_l = block_scan<kPlanThreads>(nlong, wave_tot[1]);
-  const int inc_s = block_scan<kPlanThreads>(nshort, wave_tot[2]);
-  int base = inc_c - local;
-  int lpos = inc_l - nlong, spos = inc_s - nshort;
-  int total_c = 0, total_l = 0, total_s = 0;
-  for (int j = 0; j < kPlanThreads / 64; ++j) {
-    total_c += wave_tot[0][j];
-    total_l += wave_tot[1][j];
-    total_s += wave_tot[2][j];
-  }
-  const int total = min(total_c, R);
-  int* long_list = lists + 2;
-  int* short_list = lists + 2 + num_seqs;
-  if (tid == 0) {
-    lists[0] = total_l;
-    lists[1] = total_s;
-  }
-  for (int s = s_begin; s < s_end; ++s) {
-    long long t0, t1;
-    seq_bounds(cu, is64, s, T, t0, t1);
-    if ((t1 - t0 + kChunk - 1) / kChunk >= kLongChunks) long_list[lpos++] = s;
-    else short_list[spos++] = s;
-    rec_start[s] = base;
     // overlapping (non-monotonic) cu_seqlens can ask for more than R records:
     // records past the capacity are dropped and the consumer skips them
     for (long long c0 = t0; c0 < t1; c0 += kChunk, ++base) {
@@ -179,7 +558,7 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
       if (base < R) recs[base] = make_int4(s, static_cast<int>(c0), len, 0);
     }
   }
-  if (tid == 0) rec_start[num_seqs] = total;
+  const int total = min(total_recs, R);
   for (int r = total + tid; r < R; r += kPlanThreads) recs[r] = make_int4(-1, 0, 0, 0);
 }
 
@@ -252,21 +631,17 @@ __device__ __forceinline__ void block_store(float* Z, const f32x4& v, float sc, 
 // Record r of a batch of at most kFusedPlanSeqs sequences (one per thread),
 // found by the work-group itself (no plan launch): exclusive scan of
 // per-sequence chunk counts; the thread owning the sequence that contains r
-// publishes it.  The work-group of record 0 also writes rec_start and the
-// long / short sequence lists for the consumer, as plan_kernel does.  Returns
-// false when record r does not exist.
+// publishes it.  Returns false when record r does not exist.  scratch: 32 ints.
 constexpr int kFusedPlanSeqs = kPrepassThreads;   // larger batches: a plan launch is cheaper
+static_assert(kPlanScratch <= kGva * kChunk * kMRow, "planner scratch must fit in N's space");
 
-__device__ bool find_record(int r, bool bookkeeping, const void* __restrict__ cu, int is64, int num_seqs,
-                            long long T, int R, int* __restrict__ rec_start, int* __restrict__ lists,
+__device__ bool find_record(int r, const void* __restrict__ cu, int is64, int num_seqs, long long T,
                             int* scratch, long long& t0_out, int& c_out) {
   // num_seqs <= kPrepassThreads: thread s owns sequence s (one read of its bounds)
   const int tid = threadIdx.x;
-  constexpr int kWaves = kPrepassThreads / 64;
   long long t0 = 0, t1 = 0;
   if (tid < num_seqs) seq_bounds(cu, is64, tid, T, t0, t1);
   const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
-  const int is_long = nch >= kLongChunks ? 1 : 0;
   if (tid == 0) scratch[0] = -1;
   const int inc = block_scan<kPrepassThreads>(nch, scratch + 16);
   const int base = inc - nch;
@@ -275,27 +650,6 @@ __device__ bool find_record(int r, bool bookkeeping, const void* __restrict__ cu
     scratch[0] = static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0));
     scratch[2] = static_cast<int>(c0 & 0xffffffffLL);
     scratch[3] = static_cast<int>(c0 >> 32);
-  }
-  if (bookkeeping) {
-    const int in_batch = tid < num_seqs ? 1 : 0;
-    const int inc_l = block_scan<kPrepassThreads>(is_long & in_batch, scratch + 32);
-    const int inc_s = block_scan<kPrepassThreads>((1 - is_long) & in_batch, scratch + 48);
-    if (tid < num_seqs) {
-      rec_start[tid] = base;
-      if (is_long) lists[2 + inc_l - 1] = tid;
-      else lists[2 + num_seqs + inc_s - 1] = tid;
-    }
-    if (tid == 0) {
-      int tc = 0, tl = 0, ts = 0;
-      for (int j = 0; j < kWaves; ++j) {
-        tc += scratch[16 + j];
-        tl += scratch[32 + j];
-        ts += scratch[48 + j];
-      }
-      lists[0] = tl;
-      lists[1] = ts;
-      rec_start[num_seqs] = min(tc, R);
-    }
   }
   __syncthreads();
   c_out = scratch[0];
@@ -312,20 +666,28 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const int4* __restrict__ recs, const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
-    int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
+    int gcap, int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
     uint16_t* __restrict__ ws_frag, float* __restrict__ ws_gam) {
   __shared__ PrepassSmem sm;
-  const int r = blockIdx.x / kQKHeads;
-  const int hq = blockIdx.x % kQKHeads;
   int c;
   long long t0;
+  int r, hq;
   if (fused_plan) {
-    // N's space is free until the grams; it holds the record search scratch
-    if (!find_record(r, blockIdx.x == 0, cu, is64, num_seqs, T, R, rec_start, lists,
-                     reinterpret_cast<int*>(&sm.nm[0][0][0]), t0, c))
+    // work-group 0 plans the batch (lists for the consumer) while the others
+    // run the records; N's space holds the scratch
+    if (blockIdx.x == 0) {
+      int total_recs;
+      plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists,
+                                  reinterpret_cast<int*>(&sm.nm[0][0][0]), total_recs);
       return;
+    }
+    r = (blockIdx.x - 1) / kQKHeads;
+    hq = (blockIdx.x - 1) % kQKHeads;
+    if (!find_record(r, cu, is64, num_seqs, T, reinterpret_cast<int*>(&sm.nm[0][0][0]), t0, c)) return;
     __syncthreads();   // scratch read by every thread before N is written
   } else {
+    r = blockIdx.x / kQKHeads;
+    hq = blockIdx.x % kQKHeads;
     const int4 rec = recs[r];
     c = rec.z;
     if (c <= 0) return;
@@ -879,7 +1241,6 @@ __device__ __forceinline__ void full_head_items(
 // flight) and B3 at the chunk's end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
 // side wave reads them before B2 of chunk i+1, so one buffer suffices.
 constexpr int kSplitThreads = 512;
-constexpr int kConsumerGroups = 256;     // persistent work-groups per consumer kind (one per CU)
 constexpr int kHalfV = 64;                 // value rows per split work-group (4 tiles)
 
 struct __align__(16) SplitSmem {
@@ -944,7 +1305,7 @@ __device__ __forceinline__ SplitDmaLane split_dma_lane(int ws, int lane, int hv)
 // Rows t >= c fall outside the K / Q / V resources and arrive as zeros.
 template <int P>
 __device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, const SplitDmaLane& dl, int ws,
-                                          int h, int hq, const uint16_t* __restrict__ q,
+                                          int h, int hq, bool zero_v, const uint16_t* __restrict__ q,
                                           const uint16_t* __restrict__ k,
                                           const uint16_t* __restrict__ v,
                                           const uint16_t* __restrict__ ws_frag,
@@ -958,8 +1319,9 @@ __device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, con
     dma16_buf(kr, dl.kq[j], &sm.ks[P][16 * j + 4 * ws][0]);
     dma16_buf(qr, dl.kq[j], &sm.qs[P][16 * j + 4 * ws][0]);
   }
+  // an M-run reads V = 0: an empty resource makes every V copy a zero fill
   const __amdgpu_buffer_rsrc_t vr = buf_rsrc(v + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
-                                             static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
+                                             zero_v ? 0u : static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
 #pragma unroll
   for (int j = 0; j < 2; ++j) dma16_buf(vr, dl.v[j], &sm.vs[P][32 * j + 8 * ws][0]);
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
@@ -1112,19 +1474,39 @@ __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, floa
   }
 }
 
-// Split consumer over the long-sequence list: work item = (list entry, half,
-// v-head) as entry * 16 + half * 8 + h, item i on work-group wg = i mod nwg
-// (multiples of 8 apart: v-head h runs on XCD h, both halves share its L2).
+// Split consumer over the run list: work item = (run, value half, v-head) as
+// run * 16 + half * 8 + h.  Runs come longest first; the items are dealt to
+// the work-groups in rounds of nwg, every other round in reverse order, so a
+// group that drew one of the shorter items of a round draws one of the longer
+// items of the next.  A run covers chunks [seg L, min(nch, (seg + 1) L)) of
+// its sequence:
+//   segment 0           : initial state from `state`, outputs to `out`;
+//   B-run, segment >= 1 : zero initial state, outputs O0 to `out`;
+//   M-run, segment >= 1 : identity initial state, V = 0, outputs OI to `oi`.
+// Final state: new_state for a one-segment sequence, else the segment's slot
+// (B-runs and segment 0 in slotb, row-major; M-runs in slotm as the bf16 hi /
+// lo MFMA fragments of M^T the scan multiplies with).
 __device__ __forceinline__ void split_items(
-    SplitSmem& sm, int wg, int nwg, const int* __restrict__ list, int nseq,
+    SplitSmem& sm, int wg, int nwg, const ListView lv,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const float* __restrict__ state, const void* __restrict__ cu, int is64, long long T, int R, float scale,
-    const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
-    uint16_t* __restrict__ out, float* __restrict__ new_state) {
-  for (int item = wg; item < nseq * 2 * kVHeads; item += nwg) {
+    const float* __restrict__ state, float scale, const uint16_t* __restrict__ ws_frag,
+    const float* __restrict__ ws_gam,
+    uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
+    float* __restrict__ slotb, uint16_t* __restrict__ slotm) {
+  const int nitems = lv.hdr[0] * 2 * kVHeads;
+  for (int round = 0;; ++round) {
+  const int item = round * nwg + ((round & 1) ? nwg - 1 - wg : wg);
+  if (item >= nitems) break;
   const int h = item & 7;
   const int hv = (item >> 3) & 1;
-  const int s = list[item >> 4];
+  const int4 ra = lv.runs[2 * (item >> 4)];
+  const int4 rb = lv.runs[2 * (item >> 4) + 1];
+  const int s = ra.x, slot = ra.z, rfirst = ra.w;
+  const bool mrun = (ra.y & kRunM) != 0;
+  const bool from_state = (ra.y & kRunFromState) != 0;
+  const int last_tok = min(ra.y >> 8, kChunk);   // the chunk length indexes 64-entry LDS rows
+  const long long c0r = static_cast<long long>(static_cast<unsigned>(rb.x)) | (static_cast<long long>(rb.y) << 32);
+  const int n = rb.z, nrun = rb.w;
   const int hq = h / kGva;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1133,72 +1515,63 @@ __device__ __forceinline__ void split_items(
   const int lane = tid & 63;
   const int l16 = lane & 15, lg = lane >> 4;
   const int vcol = kHalfV * hv + 16 * wt;
-
-  long long t0, t1;
-  seq_bounds(cu, is64, s, T, t0, t1);
-  const size_t st_off = ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim + 8 * lg;
-  auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
-  if (t1 <= t0) {   // empty sequence: the reference leaves new_state zero
-    if (chain) {
-#pragma unroll
-      for (int kt = 0; kt < 8; ++kt)
-        *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-    continue;
-  }
-  const int rec0 = rec_start[s];
-  const long long nchunks = (t1 - t0 + kChunk - 1) / kChunk;
-  const long long nvalid = rec0 >= R ? 0 : min(nchunks, static_cast<long long>(R - rec0));
-  auto chunk_ref = [&](long long idx) {
-    const long long c0 = t0 + idx * kChunk;
-    return ChunkRef{c0, static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0)),
-                    rec0 + static_cast<int>(idx)};
+  auto chunk_ref = [&](int li) {
+    return ChunkRef{c0r + static_cast<long long>(li) * kChunk, li == nrun - 1 ? last_tok : kChunk, rfirst + li};
   };
+  auto kappa = [&](int kt, int rr) { return 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1) + rr; };
 
   f32x4 st[8];
-  if (chain && state != nullptr) {
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(state + st_off + kappa0(kt));
-  } else {
+  for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (chain) {
+    if (mrun) {
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) st[kt][rr] = kappa(kt, rr) == vcol + l16 ? 1.0f : 0.0f;
+    } else if (from_state && state != nullptr) {
+      const float* sp = state + ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim;
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(sp + kappa(kt, 0));
+    }
   }
+  uint16_t* obase = mrun ? oi : out;
   const uint32_t ocol = 2u * static_cast<uint32_t>(vcol + 4 * lg);
   auto out_rsrc = [&](const ChunkRef& cr) {
-    return buf_rsrc(out + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
+    return buf_rsrc(obase + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
                     static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
   };
   const SplitDmaLane dl = split_dma_lane(wt, lane, hv);
 
-  if (nvalid > 0) {
+  if (n > 0) {
     if (chain) {
       bf16x8 sb[4];
       state_frags(st, sb);
 #pragma unroll
       for (int d = 0; d < 4; ++d) sm.sbx[wt][d][lane] = __builtin_bit_cast(u32x4, sb[d]);
     } else {
-      split_dma<0>(sm, chunk_ref(0), dl, wt, h, hq, q, k, v, ws_frag, ws_gam);
+      split_dma<0>(sm, chunk_ref(0), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
     }
     __syncthreads();
-    for (long long i = 0; i < nvalid; i += 2) {
+    for (int i = 0; i < n; i += 2) {
       {
         const ChunkRef cr = chunk_ref(i);
         if (chain) {
           chain_chunk<0>(sm, cr.c, st, wt, lane);
         } else {
           side_chunk<0>(sm, wt, lane, scale, out_rsrc(cr), ocol, [&] {
-            if (i + 1 < nvalid) split_dma<1>(sm, chunk_ref(i + 1), dl, wt, h, hq, q, k, v, ws_frag, ws_gam);
+            if (i + 1 < n) split_dma<1>(sm, chunk_ref(i + 1), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
           });
         }
         __syncthreads();   // B3: buffer 0 free, buffer 1 landed
       }
-      if (i + 1 < nvalid) {
+      if (i + 1 < n) {
         const ChunkRef cr = chunk_ref(i + 1);
         if (chain) {
           chain_chunk<1>(sm, cr.c, st, wt, lane);
         } else {
           side_chunk<1>(sm, wt, lane, scale, out_rsrc(cr), ocol, [&] {
-            if (i + 2 < nvalid) split_dma<0>(sm, chunk_ref(i + 2), dl, wt, h, hq, q, k, v, ws_frag, ws_gam);
+            if (i + 2 < n) split_dma<0>(sm, chunk_ref(i + 2), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
           });
         }
         __syncthreads();
@@ -1207,15 +1580,41 @@ __device__ __forceinline__ void split_items(
   }
 
   if (chain) {
+    if (slot < 0 || !mrun) {
+      float* dst = slot < 0 ? new_state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState
+                            : slotb + (static_cast<size_t>(slot) * kVHeads + h) * kHeadState;
+      dst += static_cast<size_t>(vcol + l16) * kDim;
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = st[kt];
+      for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(dst + kappa(kt, 0)) = st[kt];
+    } else {
+      // M^T fragments: element (k, k') of M^T goes to fragment (k >> 4, d), lane
+      // 16 lg' + (k & 15), slot s with k' = perm_depth(d, lg', s).  This wave
+      // holds k' = vcol + l16: d = vcol / 32, lg' = l16 / 4, s = 4 (vcol / 16 & 1) + l16 % 4.
+      uint16_t* mb = slotm + (static_cast<size_t>(slot) * kVHeads + h) * kMSlotElems;
+      const int d = vcol >> 5;
+      const int sidx = 4 * ((vcol >> 4) & 1) + (l16 & 3);
+      const int lgp = l16 >> 2;
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int kk = kappa(kt, rr);
+          const float x = st[kt][rr];
+          const uint16_t hi = f2bf(x);
+          const uint16_t lo = f2bf(x - bf2f(hi));
+          const size_t e = ((static_cast<size_t>((kk >> 4) * 4 + d) * 2 * 64) + 16 * lgp + (kk & 15)) * 8 + sidx;
+          mb[e] = hi;
+          mb[e + 512] = lo;
+        }
+      }
+    }
   }
   }
 }
 
 // Consumer entry: work-groups [0, g_long) run the split consumer over the
-// long-sequence list, the rest the full-head consumer over the short list, so
-// both regimes of a mixed batch run concurrently.  Lists come from plan_kernel
+// run list, the rest the full-head consumer over the short-sequence list, so
+// both regimes of a mixed batch run concurrently.  Lists come from the plan
 // (no host synchronisation); an empty list costs one short round of groups.
 union ConsumerLds {
   ConsumerSmem full;
@@ -1225,18 +1624,213 @@ union ConsumerLds {
 __global__ __launch_bounds__(kSplitThreads)
 void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                      const uint16_t* __restrict__ v, const float* __restrict__ state,
-                     const void* __restrict__ cu, int is64, long long T, int R, float scale,
-                     const int* __restrict__ rec_start, const int* __restrict__ lists, int num_seqs,
+                     const void* __restrict__ cu, int is64, long long T, int R, int gcap, float scale,
+                     const int* __restrict__ rec_start, int* __restrict__ lists, int num_seqs,
                      int g_long, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
-                     uint16_t* __restrict__ out, float* __restrict__ new_state) {
+                     uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
+                     float* __restrict__ slotb, uint16_t* __restrict__ slotm) {
   __shared__ ConsumerLds sm;
   const int bid = blockIdx.x;
+  const ListView lv = list_view(lists, num_seqs, gcap);
   if (bid < g_long) {
-    split_items(sm.split, bid, g_long, lists + 2, lists[0], q, k, v, state, cu, is64, T, R, scale, rec_start,
-                ws_frag, ws_gam, out, new_state);
+    split_items(sm.split, bid, g_long, lv, q, k, v, state, scale, ws_frag, ws_gam, out, new_state, oi, slotb,
+                slotm);
   } else {
-    full_head_items(sm.full, bid - g_long, static_cast<int>(gridDim.x) - g_long, lists + 2 + num_seqs, lists[1],
+    full_head_items(sm.full, bid - g_long, static_cast<int>(gridDim.x) - g_long, lv.shorts, lv.hdr[1],
                     q, k, v, state, cu, is64, T, R, scale, rec_start, ws_frag, ws_gam, out, new_state);
+  }
+}
+
+// ============================================================================
+// segment scan: S_{j+1} = S_j M_j + B_j for every multi-segment sequence
+// ============================================================================
+// One work-group per (sequence, v-head, 16 value rows); the rows of S evolve
+// independently.  Formed transposed, D = M^T S^T: the A operand is M^T (bf16
+// hi / lo fragments as the M-run stored them), the B operand S^T is read from
+// the group's copy of S in LDS.  Wave w forms output k-tile w with three
+// independent MFMA chains (hi hi from B_j, hi lo, lo hi), fp32 accumulation.
+// The operands of three steps are in flight at once, so a step costs an LDS
+// round and two barriers rather than a memory latency.  The state after
+// segment j (j < last) replaces B_j in its slot, where the correction of
+// segment j + 1 reads it; the last one is the sequence's new_state.  Every
+// state that starts a segment (S_1 .. S_{nseg-1}) is also written to slotf as
+// the correction's A-operand fragments: bf16, [v-tile][d][lane] x 8 slots,
+// lane (lg, l16) slot s = S[16 v-tile + l16][32 d + 8 lg + s].
+constexpr int kScanThreads = 512;
+constexpr int kScanRow = kDim + 4;   // floats per LDS row of S
+
+struct ScanStep {
+  bf16x8 a[4][2];   // M^T fragments of this wave's k-tile: [d][hi / lo]
+  f32x4 b;          // B_j tile
+};
+
+// This wave's part (k = 16 w + 4 lg + rr of row l16 of v-tile vt) of the
+// correction fragments of one state: slot s = 4 (lg & 1) + rr of lane
+// 16 (2 (w & 1) + lg / 2) + l16 in depth chunk w / 2.
+__device__ __forceinline__ void store_corr_frag(uint16_t* __restrict__ f, int vt, int w, int lane, const f32x4& x) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int d = w >> 1, lanep = 16 * (2 * (w & 1) + (lg >> 1)) + l16;
+  *reinterpret_cast<u32x2*>(f + (static_cast<size_t>(vt * 4 + d) * 64 + lanep) * 8 + 4 * (lg & 1)) =
+      u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
+}
+
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(int* __restrict__ lists, int num_seqs, int gcap,
+                                                            float* __restrict__ slotb,
+                                                            const uint16_t* __restrict__ slotm,
+                                                            uint16_t* __restrict__ slotf,
+                                                            float* __restrict__ new_state) {
+  __shared__ float sx[16][kScanRow];
+  const ListView lv = list_view(lists, num_seqs, gcap);
+  const int nmulti = lv.hdr[3];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // output k-tile
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  for (int item = blockIdx.x; item < nmulti * kVHeads * 8; item += gridDim.x) {
+    const int4 me = lv.multi[item >> 6];
+    const int h = (item >> 3) & 7;
+    const int nseg = me.z;
+    const size_t roff = (16 * (item & 7) + l16) * static_cast<size_t>(kDim) + 16 * w + 4 * lg;
+    auto slot = [&](int j) { return (static_cast<size_t>(me.y + j) * kVHeads + h); };
+    const int vt = item & 7;
+    __syncthreads();   // the previous item's readers of sx are done
+    {
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(slotb + slot(0) * kHeadState + roff);
+      *reinterpret_cast<f32x4*>(&sx[l16][16 * w + 4 * lg]) = s1;
+      store_corr_frag(slotf + slot(0) * kFSlotElems, vt, w, lane, s1);
+    }
+    auto load = [&](int j, ScanStep& P) {
+      if (j >= nseg) return;
+      const uint16_t* mp = slotm + slot(j) * kMSlotElems + lane * 8;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+          P.a[d][hl] = *reinterpret_cast<const bf16x8*>(mp + ((w * 4 + d) * 2 + hl) * 512);
+      P.b = *reinterpret_cast<const f32x4*>(slotb + slot(j) * kHeadState + roff);
+    };
+    auto step = [&](int j, const ScanStep& P) {
+      // B fragments: slot s of chunk d is S[row][perm_depth(d, lg, s)]
+      f32x4 a0 = P.b, a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(&sx[l16][32 * d + 4 * lg]);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(&sx[l16][32 * d + 16 + 4 * lg]);
+        const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        bf16x8 sh, sl;
+        split_frag(x, sh, sl);
+        a0 = mfma16(P.a[d][0], sh, a0);
+        a1 = mfma16(P.a[d][0], sl, a1);
+        a2 = mfma16(P.a[d][1], sh, a2);
+      }
+      const f32x4 acc = a0 + (a1 + a2);
+      __syncthreads();   // every wave has read S_j
+      *reinterpret_cast<f32x4*>(&sx[l16][16 * w + 4 * lg]) = acc;
+      if (j + 1 < nseg) {
+        *reinterpret_cast<f32x4*>(slotb + slot(j) * kHeadState + roff) = acc;
+        store_corr_frag(slotf + slot(j) * kFSlotElems, vt, w, lane, acc);
+      } else {
+        *reinterpret_cast<f32x4*>(new_state + (static_cast<size_t>(me.x) * kVHeads + h) * kHeadState + roff) = acc;
+      }
+      __syncthreads();   // S_{j+1} complete
+    };
+    ScanStep P0, P1, P2;
+    load(1, P0);
+    load(2, P1);
+    load(3, P2);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    for (int j = 1; j < nseg; j += 3) {
+      step(j, P0);
+      load(j + 3, P0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 1 < nseg) {
+        step(j + 1, P1);
+        load(j + 4, P1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (j + 2 < nseg) {
+        step(j + 2, P2);
+        load(j + 5, P2);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+}
+
+// ============================================================================
+// output correction: O = O0 + OI S_j^T for the chunks of segments >= 1
+// ============================================================================
+// One work-group per (chunk of a segment >= 1, v-head).  The state before the
+// segment, as the bf16 A fragments the scan wrote (32 KB), is copied straight
+// into LDS; wave w forms the 16 tokens 16 w .. 16 w + 15 for all 128 value
+// rows: D[v][t] = sum_k' S[v][k'] OI[t][k'], then out = bf16(O0 + D).  S
+// enters as a single bf16, as it does in Q S^T of the chunk recurrence.  The
+// wave's OI and O0 loads are issued with the copies; rows past the chunk end
+// fall outside the buffer resources (loads read 0, stores dropped).
+constexpr int kCorrThreads = 256;
+
+__global__ __launch_bounds__(kCorrThreads) void correct_kernel(int* __restrict__ lists, int num_seqs, int gcap,
+                                                               const uint16_t* __restrict__ slotf,
+                                                               const uint16_t* __restrict__ oi,
+                                                               uint16_t* __restrict__ out) {
+  __shared__ u32x4 sfrag[8][4][64];   // [v-tile][d][lane]
+  const ListView lv = list_view(lists, num_seqs, gcap);
+  const int nsegs = lv.hdr[4], L = lv.hdr[2];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  for (int item = blockIdx.x; item < nsegs * L * kVHeads; item += gridDim.x) {
+    const int h = item & 7, u = item >> 3;
+    const int4 sg = lv.segs[u / L];
+    const int ci = u % L;                         // chunk within the segment
+    if (ci * kChunk >= sg.z) continue;            // past a short last segment
+    const long long c0 = (static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32)) +
+                         static_cast<long long>(ci) * kChunk;
+    const int c = min(kChunk, sg.z - ci * kChunk);
+    __syncthreads();   // the previous item's readers of sfrag are done
+    {
+      // 32 KB: 8 copies of 1 KB per wave
+      const char* fsrc = reinterpret_cast<const char*>(slotf + (static_cast<size_t>(sg.w) * kVHeads + h) * kFSlotElems);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int blk = 8 * w + i;
+        dma16(fsrc + blk * 1024 + lane * 16, reinterpret_cast<char*>(&sfrag[0][0][0]) + blk * 1024);
+      }
+    }
+    const size_t rowbase = (static_cast<size_t>(c0) * kVHeads + h) * kDim;
+    const uint32_t bytes = static_cast<uint32_t>(c) * (kVHeads * kDim * 2);
+    const __amdgpu_buffer_rsrc_t orc = buf_rsrc(out + rowbase, bytes);
+    const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
+    const uint32_t trow = static_cast<uint32_t>(16 * w + l16) * (kVHeads * kDim * 2);
+    bf16x8 b[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      b[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
+    u32x2 o0[8];
+#pragma unroll
+    for (int vt = 0; vt < 8; ++vt) o0[vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();   // waits for every load of the group, the copies into LDS included
+#pragma unroll
+    for (int vh = 0; vh < 2; ++vh) {
+      // four independent accumulators (value tiles 4 vh .. 4 vh + 3)
+      f32x4 acc[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[e] = mfma16(__builtin_bit_cast(bf16x8, sfrag[4 * vh + e][d][lane]), b[d], acc[e]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int vt = 4 * vh + e;
+        const u32x2 o = o0[vt];
+        const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[e][0], bf_hi(o.x) + acc[e][1]),
+                          pack_bf2(bf_lo(o.y) + acc[e][2], bf_hi(o.y) + acc[e][3])};
+        __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
+      }
+    }
   }
 }
 
@@ -1265,7 +1859,10 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
   if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
   const long long R = max_records(num_seqs, total_tokens);
-  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * 2 > 0x7fffffffLL)
+  const long long gcap = max_segments(total_tokens);
+  // every work-item index (records x heads, runs x 16, multi-segment entries x 64) fits an int
+  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * 8 > 0x7fffffffLL ||
+      max_runs(num_seqs, gcap) * 2 * kVHeads > 0x7fffffffLL)
     return GDN_ERR_INVALID_ARGUMENT;
   const WsLayout L = ws_layout(num_seqs, total_tokens);
   if (workspace_bytes < L.total) return GDN_ERR_WORKSPACE_TOO_SMALL;
@@ -1277,6 +1874,10 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   auto* rec_start = reinterpret_cast<int*>(ws + L.start_off);
   auto* lists = reinterpret_cast<int*>(ws + L.list_off);
   auto* recs = reinterpret_cast<int4*>(ws + L.rec_off);
+  auto* slotb = reinterpret_cast<float*>(ws + L.slotb_off);
+  auto* slotm = reinterpret_cast<uint16_t*>(ws + L.slotm_off);
+  auto* slotf = reinterpret_cast<uint16_t*>(ws + L.slotf_off);
+  auto* oi = reinterpret_cast<uint16_t*>(ws + L.oi_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const auto* qb = static_cast<const uint16_t*>(q);
   const auto* kb = static_cast<const uint16_t*>(k);
@@ -1284,23 +1885,34 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   const auto* ab = static_cast<const uint16_t*>(a);
   const auto* bb = static_cast<const uint16_t*>(b);
   auto* ob = static_cast<uint16_t*>(output);
+  const int Ri = static_cast<int>(R), gc = static_cast<int>(gcap);
 
   // small batches: every prepass work-group finds its own record (one launch
   // fewer); large ones: a separate plan launch numbers the records once
   const int fused_plan = num_seqs <= kFusedPlanSeqs ? 1 : 0;
   if (!fused_plan)
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
-                                                        total_tokens, static_cast<int>(R), rec_start,
-                                                        recs, lists);
-  prepass_kernel<<<dim3(static_cast<unsigned>(R * kQKHeads)), dim3(kPrepassThreads), 0, st>>>(
+                                                        total_tokens, Ri, gc, rec_start, recs, lists);
+  prepass_kernel<<<dim3(static_cast<unsigned>(R * kQKHeads + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
       qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
-      static_cast<int>(R), fused_plan, rec_start, lists, frag, gam);
-  // persistent grids: one work-group per CU per consumer kind at most
-  const long long g_long = std::min<long long>(static_cast<long long>(num_seqs) * 2 * kVHeads, kConsumerGroups);
+      Ri, gc, fused_plan, rec_start, lists, frag, gam);
+  // persistent grids: one work-group per CU per consumer kind at most; a
+  // sequence needs 2 chunks (65 tokens) to be long
+  const long long g_long =
+      total_tokens > kChunk ? std::min<long long>(max_runs(num_seqs, gcap) * 2 * kVHeads, kConsumerGroups) : 0;
   const long long g_short = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads, kConsumerGroups);
   consumer_kernel<<<dim3(static_cast<unsigned>(g_long + g_short)), dim3(kSplitThreads), 0, st>>>(
-      qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, static_cast<int>(R), scale,
-      rec_start, lists, num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state);
+      qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, Ri, gc, scale, rec_start, lists,
+      num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm);
+  // a second segment needs more than kMinSegChunks chunks in one sequence
+  if (total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
+    const long long g_scan = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads * 8, 512);
+    scan_kernel<<<dim3(static_cast<unsigned>(g_scan)), dim3(kScanThreads), 0, st>>>(lists, num_seqs, gc, slotb,
+                                                                                     slotm, slotf, new_state);
+    const long long g_corr = std::min<long long>(R * kVHeads, 1024);
+    correct_kernel<<<dim3(static_cast<unsigned>(g_corr)), dim3(kCorrThreads), 0, st>>>(lists, num_seqs, gc, slotf,
+                                                                                        oi, ob);
+  }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
 }

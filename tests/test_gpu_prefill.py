@@ -42,6 +42,38 @@ def test_prefill_ragged(gpu, lengths):
            f"prefill ragged {lengths}")
 
 
+@pytest.mark.parametrize("lengths", [[2048, 100], [1500, 0, 333, 1000, 64], [4096], [700, 3000, 65, 1300]])
+def test_prefill_segmented(gpu, lengths):
+    # long sequences are cut into segments that run concurrently (zero-state
+    # and identity-state runs) and are stitched by the scan and the correction
+    _check(prefill_inputs_from_lengths(lengths, seed=sum(lengths) % 1000), gpu,
+           f"prefill segmented {lengths}")
+
+
+@pytest.mark.parametrize("lengths", [[3000, 1500, 700], [4096]])
+def test_prefill_segmented_weak_decay(gpu, lengths):
+    # with the default gate distribution the state forgets a segment's start
+    # within a few chunks (the segment maps M_j vanish); near-1 decay keeps
+    # M_j large, so the scan and the state before every segment matter
+    p = prefill_inputs_from_lengths(lengths, seed=len(lengths) + 40)
+    p.A_log = torch.linspace(-8.0, -5.0, 8)
+    _check(p, gpu, f"prefill segmented weak decay {lengths}")
+
+
+def test_prefill_large_batch_plan_launch(gpu):
+    # more sequences than one planning work-group owns: the separate plan
+    # launch numbers the records; one long sequence is still segmented
+    lengths = [int(x) for x in torch.randint(1, 130, (599,), generator=torch.Generator().manual_seed(5))]
+    lengths[300] = 2500
+    _check(prefill_inputs_from_lengths(lengths, seed=77), gpu, "prefill 600 sequences (plan launch)")
+
+
+def test_prefill_segmented_state_none(gpu):
+    p = prefill_inputs_from_lengths([1800, 900], seed=21)
+    p.state = None
+    _check(p, gpu, "prefill segmented state=None")
+
+
 def test_prefill_state_none_and_int64(gpu):
     p = prefill_inputs_from_lengths([90, 17, 64], seed=3, cu_dtype=torch.int64)
     p.state = None
