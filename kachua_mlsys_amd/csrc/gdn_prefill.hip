@@ -47,6 +47,17 @@ namespace gdn {
 
 constexpr int kChunk = 64;
 constexpr int kFragElems = 4096;             // 64x64 16-bit operand in fragment order
+// Gate block per (record, v-head): gam[64], tail[64], the chunk's map bound
+// (below) at [128], padding to 256 floats (one 1 KB copy).
+constexpr int kGamStride = 4 * kChunk;
+constexpr int kBoundAt = 2 * kChunk;
+// The homogeneous part of one token's update multiplies the state by
+// g_t (I - beta_t k_t k_t^T), whose 2-norm is at most g_t max(1, |1 - beta_t |k_t|^2|).
+// The prepass stores the chunk's sum of log2 of these factors; once a run from
+// the identity (an M-run) has accumulated less than kNegligibleLog2, its state
+// and all later outputs are below 2^-60 of the state they multiply and the run
+// stops.
+constexpr float kNegligibleLog2 = -60.0f;
 constexpr int kFrags = 2;                    // per (record, v-head): Tb (fp16), Aqk (bf16)
 
 // MFMA operands in "permuted fragment order".  For v_mfma_f32_16x16x32_bf16
@@ -89,7 +100,8 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 // each), short sequences.  Everything a kernel needs about one work item sits
 // in one entry, so an item costs one dependent load before its data.
 //   hdr[0] runs, [1] short sequences, [2] segment length L (chunks),
-//   [3] multi-segment sequences, [4] segments >= 1 over all sequences
+//   [3] multi-segment sequences, [4] segments >= 1 over all sequences,
+//   [5] split-consumer work queue (items claimed past each group's first)
 //   multi[e]   = (seq, first slot, segments, 0)
 //   segs[i]    = (first token lo, hi, tokens in the segment, slot holding the
 //                 state before the segment) for every segment >= 1
@@ -128,7 +140,7 @@ __host__ __device__ inline size_t list_ints(int num_seqs, long long gcap) {
 // ---- workspace layout -------------------------------------------------------
 struct WsLayout {
   size_t frag_off;     // u16  [R][8][2][4096]   (Tb fp16, Aqk bf16)
-  size_t gam_off;      // f32  [R][8][2][64]     (gam, tail)
+  size_t gam_off;      // f32  [R][8][kGamStride] (gam, tail, map bound)
   size_t start_off;    // i32  [N + 1]           record start per sequence
   size_t list_off;     // i32  lists (see list_view)
   size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
@@ -136,6 +148,7 @@ struct WsLayout {
   size_t slotm_off;    // u16  [G][8][kMSlotElems] M_j^T fragments
   size_t slotf_off;    // u16  [G][8][kFSlotElems] state before segment j as correction fragments
   size_t oi_off;       // u16  [T][8][128]       M-run outputs OI (rows of segments >= 1)
+  size_t mval_off;     // i32  [G][8]            chunks of each M-run whose outputs OI were formed
   size_t total;
 };
 
@@ -152,7 +165,7 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   const size_t N = static_cast<size_t>(num_seqs);
   size_t off = 0;
   L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kFragElems * sizeof(uint16_t));
-  L.gam_off = off;   off = align256(off + R * kVHeads * 2 * kChunk * sizeof(float));
+  L.gam_off = off;   off = align256(off + R * kVHeads * kGamStride * sizeof(float));
   L.start_off = off; off = align256(off + (N + 1) * sizeof(int));
   L.list_off = off;  off = align256(off + list_ints(num_seqs, static_cast<long long>(G)) * sizeof(int));
   L.rec_off = off;   off = align256(off + R * sizeof(int4));
@@ -160,6 +173,7 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   L.slotm_off = off; off = align256(off + G * kVHeads * kMSlotElems * sizeof(uint16_t));
   L.slotf_off = off; off = align256(off + G * kVHeads * kFSlotElems * sizeof(uint16_t));
   L.oi_off = off;    off = align256(off + static_cast<size_t>(tokens) * kVHeads * kDim * sizeof(uint16_t));
+  L.mval_off = off;  off = align256(off + G * kVHeads * sizeof(int));
   L.total = off;
   return L;
 }
@@ -212,6 +226,22 @@ __device__ __forceinline__ int wave_incl_sum(int x) {
 }
 
 __device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_incl_sum(x), 63); }
+
+// Sum over the 64 lanes (fp32, every lane gets it): DPP within rows of 16, then
+// the four row totals.
+template <int CTRL>
+__device__ __forceinline__ float dppf0(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ __forceinline__ float wave_sumf(float x) {
+  x += dppf0<0x111>(x);
+  x += dppf0<0x112>(x);
+  x += dppf0<0x114>(x);
+  x += dppf0<0x118>(x);
+  auto lane_f = [&](int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l)); };
+  return (lane_f(15) + lane_f(31)) + (lane_f(47) + lane_f(63));
+}
 
 // Maximum over the lanes of non-negative values (0 is the identity).
 __device__ __forceinline__ int wave_max0(int x) {
@@ -472,6 +502,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       lv.hdr[2] = L;
       lv.hdr[3] = tot[2];
       lv.hdr[4] = tot[3] - tot[2];
+      lv.hdr[5] = 0;
       rec_start[num_seqs] = min(tot[0], R);
     }
   }
@@ -595,7 +626,7 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
 constexpr int kPrepassThreads = 512;   // 8 waves: waves 0-3 serve v-head 2hq, waves 4-7 v-head 2hq+1
 constexpr int kMRow = 68;     // floats per LDS row of the 64x64 fp32 matrices (16-byte aligned)
 
-// 70.6 KB: two work-groups (four v-heads' worth) per CU.  The T matrices reuse
+// 71.2 KB: two work-groups (four v-heads' worth) per CU.  The T matrices reuse
 // the K / Q rows' space once the grams have been formed.
 struct __align__(16) PrepassSmem {
   union {
@@ -605,6 +636,7 @@ struct __align__(16) PrepassSmem {
   float nm[kGva][kChunk][kMRow];    // N = strict lower beta_t rho K K^T; upper blocks are scratch
   float lgam[kGva][kChunk];         // Gam_t / ln 2 (log2 cumulative decay)
   float beta[kGva][kChunk];
+  float kb2[kGva][kChunk];          // log2 max(1, |1 - beta_t |k_t|^2|)
 };
 
 // j-th lower 16x16 tile (mi >= ni) of a 4x4 tile grid, row by row:
@@ -745,7 +777,7 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     sm.lgam[hh][t] = scan;
     sm.beta[hh][t] = bet;
     const float last = __shfl(scan, c - 1, 64);
-    float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * 2 * kChunk;
+    float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * kGamStride;
     gp[t] = t < c ? fast_exp2(scan) : 0.0f;
     gp[kChunk + t] = t < c ? fast_exp2(last - scan) : 0.0f;
   }
@@ -795,6 +827,8 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
         for (int rr = 0; rr < 4; ++rr) {
           const int t = 16 * mi + 4 * lg + rr;
           sm.nm[e][t][i] = i < t ? bt[rr] * fast_exp2(gt[rr] - gi_) * akk[n][rr] : 0.0f;
+          // diagonal: |k_t|^2 (rows t >= c have beta = 0 and contribute 0)
+          if (i == t) sm.kb2[e][t] = __log2f(fmaxf(1.0f, fabsf(1.0f - bt[rr] * akk[n][rr])));
         }
       }
       {
@@ -823,6 +857,12 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
         u32x2{0u, 0u};
   }
   __syncthreads();   // N complete; K / Q space becomes T
+
+  // the chunk's map bound: sum over tokens of log2 g_t + log2 max(1, |1 - beta_t |k_t|^2|)
+  if (wl == 0) {
+    const float lb = wave_sumf(sm.kb2[hh][lane]) + sm.lgam[hh][c - 1];
+    if (lane == 0) ws_gam[(static_cast<size_t>(r) * kVHeads + h) * kGamStride + kBoundAt] = lb;
+  }
 
   // ---- T = (I + N)^{-1} per v-head: diagonal 16x16 blocks by forward substitution ----
   float (*nmh)[kMRow] = sm.nm[hh];
@@ -1004,8 +1044,8 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
 #pragma unroll
   for (int j = 0; j < kFrags; ++j)
     dma16(fb + (512 * j + 64 * w + lane) * 16, &sm.frag[P][0][0] + (512 * j + 64 * w) * 8);
-  if (w == 0)   // gam and tail are contiguous (512 bytes); lanes 32..63 fill the padding
-    dma16(reinterpret_cast<const char*>(ws_gam + rh * 2 * kChunk) + 16 * (lane & 31), &sm.gt[P][0]);
+  if (w == 0)   // gam, tail and the map bound: one 1 KB block
+    dma16(reinterpret_cast<const char*>(ws_gam + rh * kGamStride) + 16 * lane, &sm.gt[P][0]);
 }
 
 // One chunk of the recurrence for the 16-wide V tile of this wave.
@@ -1251,6 +1291,7 @@ struct __align__(16) SplitSmem {
   float gt[2][4 * kChunk];
   u32x4 sbx[4][4][64];                     // chain wave w: bf16 S fragments sb[d], per lane
   u32x4 dox[4][2][64];                     // chain wave w: bf16 Delta fragments dob[d], per lane
+  int next_item;                           // the group's next work item (from the queue)
 };
 
 __device__ __forceinline__ int vh_swz(int t) { return ((t >> 1) & 1) << 2; }
@@ -1283,7 +1324,7 @@ struct SplitDmaLane {
   uint32_t kq[4];     // K / Q row (kr + 16 j), source chunk of this lane
   uint32_t v[2];      // V row (vr + 32 j), this half's source chunk
   uint32_t fr;        // fragment bytes of pass 0 (+4 KB per pass)
-  uint32_t g;         // gam / tail
+  uint32_t g;         // gate block
 };
 
 __device__ __forceinline__ SplitDmaLane split_dma_lane(int ws, int lane, int hv) {
@@ -1297,7 +1338,7 @@ __device__ __forceinline__ SplitDmaLane split_dma_lane(int ws, int lane, int hv)
 #pragma unroll
   for (int j = 0; j < 2; ++j) o.v[j] = static_cast<uint32_t>(vr + 32 * j) * (kVHeads * kDim * 2) + vcol;
   o.fr = static_cast<uint32_t>(64 * ws + lane) * 16u;
-  o.g = 16u * static_cast<uint32_t>(lane & 31);
+  o.g = 16u * static_cast<uint32_t>(lane);
   return o;
 }
 
@@ -1328,7 +1369,7 @@ __device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, con
   const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kFrags * kFragElems, kFrags * kFragElems * 2);
 #pragma unroll
   for (int j = 0; j < 2 * kFrags; ++j) dma16_buf(fr, dl.fr + 4096u * j, &sm.frag[P][0][0] + (256 * j + 64 * ws) * 8);
-  if (ws == 0) dma16_buf(buf_rsrc(ws_gam + rh * 2 * kChunk, 2 * kChunk * 4), dl.g, &sm.gt[P][0]);
+  if (ws == 0) dma16_buf(buf_rsrc(ws_gam + rh * kGamStride, kGamStride * 4), dl.g, &sm.gt[P][0]);
 }
 
 // bf16 B-operand fragments of the state tile: slots of depth chunk d are
@@ -1475,11 +1516,12 @@ __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, floa
 }
 
 // Split consumer over the run list: work item = (run, value half, v-head) as
-// run * 16 + half * 8 + h.  Runs come longest first; the items are dealt to
-// the work-groups in rounds of nwg, every other round in reverse order, so a
-// group that drew one of the shorter items of a round draws one of the longer
-// items of the next.  A run covers chunks [seg L, min(nch, (seg + 1) L)) of
-// its sequence:
+// run * 16 + half * 8 + h.  Runs come longest first.  Work-group wg starts with
+// item wg; later items are claimed from a queue (a counter in the list
+// header), so a group that finishes early (a short run, an M-run that stopped)
+// takes the next longest item.  The claim is issued during the item's last
+// chunk, which hides its latency.  A run covers chunks [seg L, min(nch,
+// (seg + 1) L)) of its sequence:
 //   segment 0           : initial state from `state`, outputs to `out`;
 //   B-run, segment >= 1 : zero initial state, outputs O0 to `out`;
 //   M-run, segment >= 1 : identity initial state, V = 0, outputs OI to `oi`.
@@ -1492,11 +1534,18 @@ __device__ __forceinline__ void split_items(
     const float* __restrict__ state, float scale, const uint16_t* __restrict__ ws_frag,
     const float* __restrict__ ws_gam,
     uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
-    float* __restrict__ slotb, uint16_t* __restrict__ slotm) {
+    float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval) {
   const int nitems = lv.hdr[0] * 2 * kVHeads;
-  for (int round = 0;; ++round) {
-  const int item = round * nwg + ((round & 1) ? nwg - 1 - wg : wg);
-  if (item >= nitems) break;
+  int* queue = lv.hdr + 5;
+  for (int item = wg; item < nitems;) {
+  int claimed = 0;   // thread 0: the next item from the queue (once claimed)
+  bool has_claim = false;
+  auto claim = [&] {
+    if (threadIdx.x == 0 && !has_claim) {
+      claimed = nwg + atomicAdd(queue, 1);
+      has_claim = true;
+    }
+  };
   const int h = item & 7;
   const int hv = (item >> 3) & 1;
   const int4 ra = lv.runs[2 * (item >> 4)];
@@ -1543,6 +1592,12 @@ __device__ __forceinline__ void split_items(
   };
   const SplitDmaLane dl = split_dma_lane(wt, lane, hv);
 
+  // An M-run stops once the bound of its map falls below kNegligibleLog2: its
+  // outputs of later chunks are negligible (the correction skips them) and so
+  // is its final state.  Every wave accumulates the same bounds in the same
+  // order, so the decision is uniform.
+  float lbound = 0.0f;
+  int formed = n;   // chunks whose outputs were formed
   if (n > 0) {
     if (chain) {
       bf16x8 sb[4];
@@ -1555,6 +1610,7 @@ __device__ __forceinline__ void split_items(
     __syncthreads();
     for (int i = 0; i < n; i += 2) {
       {
+        if (i + 1 >= n) claim();
         const ChunkRef cr = chunk_ref(i);
         if (chain) {
           chain_chunk<0>(sm, cr.c, st, wt, lane);
@@ -1563,9 +1619,15 @@ __device__ __forceinline__ void split_items(
             if (i + 1 < n) split_dma<1>(sm, chunk_ref(i + 1), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
           });
         }
+        lbound += sm.gt[0][kBoundAt];
         __syncthreads();   // B3: buffer 0 free, buffer 1 landed
       }
+      if (mrun && lbound < kNegligibleLog2) {
+        formed = i + 1;
+        break;
+      }
       if (i + 1 < n) {
+        if (i + 2 >= n) claim();
         const ChunkRef cr = chunk_ref(i + 1);
         if (chain) {
           chain_chunk<1>(sm, cr.c, st, wt, lane);
@@ -1574,10 +1636,16 @@ __device__ __forceinline__ void split_items(
             if (i + 2 < n) split_dma<0>(sm, chunk_ref(i + 2), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
           });
         }
+        lbound += sm.gt[1][kBoundAt];
         __syncthreads();
+        if (mrun && lbound < kNegligibleLog2) {
+          formed = i + 2;
+          break;
+        }
       }
     }
   }
+  if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed;
 
   if (chain) {
     if (slot < 0 || !mrun) {
@@ -1609,6 +1677,10 @@ __device__ __forceinline__ void split_items(
       }
     }
   }
+  claim();
+  if (threadIdx.x == 0) sm.next_item = claimed;
+  __syncthreads();
+  item = sm.next_item;
   }
 }
 
@@ -1628,13 +1700,16 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
                      const int* __restrict__ rec_start, int* __restrict__ lists, int num_seqs,
                      int g_long, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
                      uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
-                     float* __restrict__ slotb, uint16_t* __restrict__ slotm) {
+                     float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval) {
   __shared__ ConsumerLds sm;
   const int bid = blockIdx.x;
   const ListView lv = list_view(lists, num_seqs, gcap);
   if (bid < g_long) {
     split_items(sm.split, bid, g_long, lv, q, k, v, state, scale, ws_frag, ws_gam, out, new_state, oi, slotb,
-                slotm);
+                slotm, mval);
+    // an M-run that stopped early may leave its next chunk's copies into LDS in
+    // flight: they land before the work-group releases its LDS
+    __builtin_amdgcn_s_waitcnt(0);
   } else {
     full_head_items(sm.full, bid - g_long, static_cast<int>(gridDim.x) - g_long, lv.shorts, lv.hdr[1],
                     q, k, v, state, cu, is64, T, R, scale, rec_start, ws_frag, ws_gam, out, new_state);
@@ -1766,10 +1841,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(int* __restrict__ li
 // rows: D[v][t] = sum_k' S[v][k'] OI[t][k'], then out = bf16(O0 + D).  S
 // enters as a single bf16, as it does in Q S^T of the chunk recurrence.  The
 // wave's OI and O0 loads are issued with the copies; rows past the chunk end
-// fall outside the buffer resources (loads read 0, stores dropped).
+// fall outside the buffer resources (loads read 0, stores dropped).  Chunks
+// past the point where the segment's M-run stopped (its map bound below
+// kNegligibleLog2) keep out = O0.
 constexpr int kCorrThreads = 256;
 
 __global__ __launch_bounds__(kCorrThreads) void correct_kernel(int* __restrict__ lists, int num_seqs, int gcap,
+                                                               const int* __restrict__ mval,
                                                                const uint16_t* __restrict__ slotf,
                                                                const uint16_t* __restrict__ oi,
                                                                uint16_t* __restrict__ out) {
@@ -1784,6 +1862,7 @@ __global__ __launch_bounds__(kCorrThreads) void correct_kernel(int* __restrict__
     const int4 sg = lv.segs[u / L];
     const int ci = u % L;                         // chunk within the segment
     if (ci * kChunk >= sg.z) continue;            // past a short last segment
+    if (ci >= mval[static_cast<size_t>(sg.w + 1) * kVHeads + h]) continue;   // OI negligible: out = O0
     const long long c0 = (static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32)) +
                          static_cast<long long>(ci) * kChunk;
     const int c = min(kChunk, sg.z - ci * kChunk);
@@ -1878,6 +1957,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   auto* slotm = reinterpret_cast<uint16_t*>(ws + L.slotm_off);
   auto* slotf = reinterpret_cast<uint16_t*>(ws + L.slotf_off);
   auto* oi = reinterpret_cast<uint16_t*>(ws + L.oi_off);
+  auto* mval = reinterpret_cast<int*>(ws + L.mval_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const auto* qb = static_cast<const uint16_t*>(q);
   const auto* kb = static_cast<const uint16_t*>(k);
@@ -1903,15 +1983,15 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   const long long g_short = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads, kConsumerGroups);
   consumer_kernel<<<dim3(static_cast<unsigned>(g_long + g_short)), dim3(kSplitThreads), 0, st>>>(
       qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, Ri, gc, scale, rec_start, lists,
-      num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm);
+      num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm, mval);
   // a second segment needs more than kMinSegChunks chunks in one sequence
   if (total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
     const long long g_scan = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads * 8, 512);
     scan_kernel<<<dim3(static_cast<unsigned>(g_scan)), dim3(kScanThreads), 0, st>>>(lists, num_seqs, gc, slotb,
                                                                                      slotm, slotf, new_state);
     const long long g_corr = std::min<long long>(R * kVHeads, 1024);
-    correct_kernel<<<dim3(static_cast<unsigned>(g_corr)), dim3(kCorrThreads), 0, st>>>(lists, num_seqs, gc, slotf,
-                                                                                        oi, ob);
+    correct_kernel<<<dim3(static_cast<unsigned>(g_corr)), dim3(kCorrThreads), 0, st>>>(lists, num_seqs, gc, mval,
+                                                                                        slotf, oi, ob);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
