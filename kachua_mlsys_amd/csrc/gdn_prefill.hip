@@ -30,8 +30,9 @@
 //              in MFMA registers.  Short sequences run one work-group per
 //              (sequence, v-head).  Chunk operands are copied from global
 //              memory straight into double-buffered LDS.
-//   scan     : S_{j+1} = S_j M_j + B_j over the segments of each sequence.
-//   correct  : O = O0 + OI S_j^T for the tokens of segments >= 1.
+//   finish   : the state before each segment (S_{j+1} = S_j M_j + B_j), the
+//              output correction O = O0 + OI S_j^T for segments >= 1, and the
+//              final state of multi-segment sequences.
 //
 // Precision policy (fp32 accumulation everywhere): K, Q, V are bf16 inputs, so
 // their products are exact.  S enters K S^T and Q S^T as a single bf16; Tb and
@@ -58,6 +59,7 @@ constexpr int kBoundAt = 2 * kChunk;
 // and all later outputs are below 2^-60 of the state they multiply and the run
 // stops.
 constexpr float kNegligibleLog2 = -60.0f;
+constexpr int kMNegligible = 1 << 30;   // flag in the M-run table: the run stopped early, its map is negligible
 constexpr int kFrags = 2;                    // per (record, v-head): Tb (fp16), Aqk (bf16)
 
 // MFMA operands in "permuted fragment order".  For v_mfma_f32_16x16x32_bf16
@@ -86,7 +88,6 @@ __host__ __device__ constexpr int perm_depth(int d, int lg, int s) {
 constexpr int kMinSegChunks = 4;   // shortest segment the planner may choose
 constexpr int kMaxSegChunks = 1024;   // longest finite candidate (segments of multi-segment sequences)
 constexpr int kMSlotElems = 8 * 4 * 2 * 64 * 8;   // M_j^T as bf16 hi / lo MFMA fragments, per head
-constexpr int kFSlotElems = 8 * 4 * 64 * 8;       // a state as bf16 correction fragments, per head
 
 // Upper bound on the segments of all multi-segment sequences: a sequence of
 // tau tokens split into n >= 2 segments of L >= kMinSegChunks chunks has
@@ -101,15 +102,16 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 // in one entry, so an item costs one dependent load before its data.
 //   hdr[0] runs, [1] short sequences, [2] segment length L (chunks),
 //   [3] multi-segment sequences, [4] segments >= 1 over all sequences,
-//   [5] split-consumer work queue (items claimed past each group's first)
+//   [8] split-consumer work queue (items claimed past each group's first)
 //   multi[e]   = (seq, first slot, segments, 0)
-//   segs[i]    = (first token lo, hi, tokens in the segment, slot holding the
-//                 state before the segment) for every segment >= 1
+//   segs[i]    = (first token lo, hi, tokens in the segment | j << 17, slot of
+//                 segment j - 1) for every segment j >= 1 (L <= 1024 chunks:
+//                 at most 65536 tokens)
 //   runs[2i]   = (seq, flags | tokens of the run's last chunk << 8,
 //                 final-state slot or -1 for new_state, first record)
 //   runs[2i+1] = (first token lo, hi, chunks with records, chunks)
 //   flags: kRunM (M-run), kRunFromState (initial state from `state`)
-constexpr int kListHdr = 8;
+constexpr int kListHdr = 16;
 constexpr int kRunM = 1;
 constexpr int kRunFromState = 2;
 __host__ __device__ inline long long max_runs(int num_seqs, long long gcap) { return 2 * gcap + num_seqs; }
@@ -144,11 +146,10 @@ struct WsLayout {
   size_t start_off;    // i32  [N + 1]           record start per sequence
   size_t list_off;     // i32  lists (see list_view)
   size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
-  size_t slotb_off;    // f32  [G][8][128][128]  B_j, then (after the scan) the state after segment j
+  size_t slotb_off;    // f32  [G][8][128][128]  S_1 (slot of segment 0), B_j (slots of segments j >= 1)
   size_t slotm_off;    // u16  [G][8][kMSlotElems] M_j^T fragments
-  size_t slotf_off;    // u16  [G][8][kFSlotElems] state before segment j as correction fragments
   size_t oi_off;       // u16  [T][8][128]       M-run outputs OI (rows of segments >= 1)
-  size_t mval_off;     // i32  [G][8]            chunks of each M-run whose outputs OI were formed
+  size_t mval_off;     // i32  [G][8]            M-run chunks whose outputs OI were formed | kMNegligible
   size_t total;
 };
 
@@ -171,7 +172,6 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   L.rec_off = off;   off = align256(off + R * sizeof(int4));
   L.slotb_off = off; off = align256(off + G * kVHeads * kHeadState * sizeof(float));
   L.slotm_off = off; off = align256(off + G * kVHeads * kMSlotElems * sizeof(uint16_t));
-  L.slotf_off = off; off = align256(off + G * kVHeads * kFSlotElems * sizeof(uint16_t));
   L.oi_off = off;    off = align256(off + static_cast<size_t>(tokens) * kVHeads * kDim * sizeof(uint16_t));
   L.mval_off = off;  off = align256(off + G * kVHeads * sizeof(int));
   L.total = off;
@@ -496,13 +496,13 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       ps[kPsCur + b0_] = ex;
       ps[kPsCur + b1_] = ex + h0;
     }
+    if (lane == 0) lv.hdr[8] = 0;   // work queue
     if (lane == 63) {
       lv.hdr[0] = tot[4] + inc;
       lv.hdr[1] = tot[1];
       lv.hdr[2] = L;
       lv.hdr[3] = tot[2];
       lv.hdr[4] = tot[3] - tot[2];
-      lv.hdr[5] = 0;
       rec_start[num_seqs] = min(tot[0], R);
     }
   }
@@ -531,8 +531,8 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       for (int j = 1; j < p.nseg; ++j) {
         const long long c0 = t0 + static_cast<long long>(j) * L * kChunk;
         const int tok = static_cast<int>(min(t1 - c0, static_cast<long long>(L) * kChunk));
-        lv.segs[gb - mp + j - 1] =
-            make_int4(static_cast<int>(c0 & 0xffffffffLL), static_cast<int>(c0 >> 32), tok, gb + j - 1);
+        lv.segs[gb - mp + j - 1] = make_int4(static_cast<int>(c0 & 0xffffffffLL), static_cast<int>(c0 >> 32),
+                                             tok | (j << 17), gb + j - 1);
       }
       ++mp;
       gb += p.nseg;
@@ -1536,7 +1536,7 @@ __device__ __forceinline__ void split_items(
     uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
     float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval) {
   const int nitems = lv.hdr[0] * 2 * kVHeads;
-  int* queue = lv.hdr + 5;
+  int* queue = lv.hdr + 8;
   for (int item = wg; item < nitems;) {
   int claimed = 0;   // thread 0: the next item from the queue (once claimed)
   bool has_claim = false;
@@ -1645,7 +1645,7 @@ __device__ __forceinline__ void split_items(
       }
     }
   }
-  if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed;
+  if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed | (formed < n ? kMNegligible : 0);
 
   if (chain) {
     if (slot < 0 || !mrun) {
@@ -1717,197 +1717,201 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 }
 
 // ============================================================================
-// segment scan: S_{j+1} = S_j M_j + B_j for every multi-segment sequence
+// finish: states before segments, output correction, final states
 // ============================================================================
-// One work-group per (sequence, v-head, 16 value rows); the rows of S evolve
-// independently.  Formed transposed, D = M^T S^T: the A operand is M^T (bf16
-// hi / lo fragments as the M-run stored them), the B operand S^T is read from
-// the group's copy of S in LDS.  Wave w forms output k-tile w with three
-// independent MFMA chains (hi hi from B_j, hi lo, lo hi), fp32 accumulation.
-// The operands of three steps are in flight at once, so a step costs an LDS
-// round and two barriers rather than a memory latency.  The state after
-// segment j (j < last) replaces B_j in its slot, where the correction of
-// segment j + 1 reads it; the last one is the sequence's new_state.  Every
-// state that starts a segment (S_1 .. S_{nseg-1}) is also written to slotf as
-// the correction's A-operand fragments: bf16, [v-tile][d][lane] x 8 slots,
-// lane (lg, l16) slot s = S[16 v-tile + l16][32 d + 8 lg + s].
-constexpr int kScanThreads = 512;
-constexpr int kScanRow = kDim + 4;   // floats per LDS row of S
+// S_{j+1} = S_j M_j + B_j and O_j = O0_j + OI_j S_j^T.  An M-run that stopped
+// early (kMNegligible) has a map below 2^-60, so the state after its segment is
+// B_j itself: the state before segment j is rebuilt from the latest such
+// segment before it (or from S_1), with scan steps only across segments whose
+// maps are not negligible.  Work items, one work-group each:
+//   (segment j >= 1, block of kFinChunks chunks, v-head): S_j, then out =
+//        bf16(O0 + OI S_j^T) for the block's chunks whose OI was formed (the
+//        rest keep O0);
+//   (multi-segment sequence, v-head): new_state = S_nseg.
+// A scan step forms D = M^T S^T on MFMA with M^T as the M-run stored it (bf16
+// hi / lo) and S split into hi / lo from LDS (three products, fp32
+// accumulation from B_i).  The correction multiplies OI (bf16) by S as a single
+// bf16, as the chunk recurrence does in Q S^T.
+constexpr int kFinThreads = 256;
+constexpr int kFinChunks = 4;
+constexpr int kFinRow = kDim + 4;   // floats per LDS row of S
 
-struct ScanStep {
-  bf16x8 a[4][2];   // M^T fragments of this wave's k-tile: [d][hi / lo]
-  f32x4 b;          // B_j tile
+union FinishLds {
+  float s[kDim][kFinRow];          // S (fp32, row-major, padded)
+  u32x4 frag[8][4][64];            // S as correction A fragments: [v-tile][d][lane], slot s = S[16 vt + l16][32 d + 8 lg + s]
 };
 
-// This wave's part (k = 16 w + 4 lg + rr of row l16 of v-tile vt) of the
-// correction fragments of one state: slot s = 4 (lg & 1) + rr of lane
-// 16 (2 (w & 1) + lg / 2) + l16 in depth chunk w / 2.
-__device__ __forceinline__ void store_corr_frag(uint16_t* __restrict__ f, int vt, int w, int lane, const f32x4& x) {
+// State before segment j of the sequence whose slots start at g0, v-head h,
+// into sm.s (fp32).
+__device__ void state_before(FinishLds& sm, int g0, int j, int h, const float* __restrict__ slotb,
+                             const uint16_t* __restrict__ slotm, const int* __restrict__ mval, int w, int lane) {
+  const int tid = threadIdx.x;
   const int l16 = lane & 15, lg = lane >> 4;
-  const int d = w >> 1, lanep = 16 * (2 * (w & 1) + (lg >> 1)) + l16;
-  *reinterpret_cast<u32x2*>(f + (static_cast<size_t>(vt * 4 + d) * 64 + lanep) * 8 + 4 * (lg & 1)) =
-      u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
-}
-
-__global__ __launch_bounds__(kScanThreads) void scan_kernel(int* __restrict__ lists, int num_seqs, int gcap,
-                                                            float* __restrict__ slotb,
-                                                            const uint16_t* __restrict__ slotm,
-                                                            uint16_t* __restrict__ slotf,
-                                                            float* __restrict__ new_state) {
-  __shared__ float sx[16][kScanRow];
-  const ListView lv = list_view(lists, num_seqs, gcap);
-  const int nmulti = lv.hdr[3];
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // output k-tile
-  const int lane = threadIdx.x & 63;
-  const int l16 = lane & 15, lg = lane >> 4;
-  for (int item = blockIdx.x; item < nmulti * kVHeads * 8; item += gridDim.x) {
-    const int4 me = lv.multi[item >> 6];
-    const int h = (item >> 3) & 7;
-    const int nseg = me.z;
-    const size_t roff = (16 * (item & 7) + l16) * static_cast<size_t>(kDim) + 16 * w + 4 * lg;
-    auto slot = [&](int j) { return (static_cast<size_t>(me.y + j) * kVHeads + h); };
-    const int vt = item & 7;
-    __syncthreads();   // the previous item's readers of sx are done
-    {
-      const f32x4 s1 = *reinterpret_cast<const f32x4*>(slotb + slot(0) * kHeadState + roff);
-      *reinterpret_cast<f32x4*>(&sx[l16][16 * w + 4 * lg]) = s1;
-      store_corr_frag(slotf + slot(0) * kFSlotElems, vt, w, lane, s1);
+  int i0 = j - 1;   // S_{i0+1} is exactly slotb[g0 + i0]: S_1, or B_{i0} after a negligible map
+  while (i0 > 0 && (mval[static_cast<size_t>(g0 + i0) * kVHeads + h] & kMNegligible) == 0) --i0;
+  {
+    // 64 KB: every load of the thread is issued before the first LDS write
+    const float* src = slotb + (static_cast<size_t>(g0 + i0) * kVHeads + h) * kHeadState;
+    constexpr int kPer = kDim * kDim / 4 / kFinThreads;
+    f32x4 t[kPer];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int q4 = tid + e * kFinThreads;
+      t[e] = *reinterpret_cast<const f32x4*>(src + (q4 >> 5) * kDim + (q4 & 31) * 4);
     }
-    auto load = [&](int j, ScanStep& P) {
-      if (j >= nseg) return;
-      const uint16_t* mp = slotm + slot(j) * kMSlotElems + lane * 8;
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int q4 = tid + e * kFinThreads;
+      *reinterpret_cast<f32x4*>(&sm.s[q4 >> 5][(q4 & 31) * 4]) = t[e];
+    }
+  }
+  __syncthreads();
+  for (int i = i0 + 1; i < j; ++i) {
+    // wave w forms output k-tiles 2w, 2w+1 for all 128 rows: D = M^T S^T; the
+    // step's operand loads are all issued before the first product
+    const size_t gh = static_cast<size_t>(g0 + i) * kVHeads + h;
+    const uint16_t* mp = slotm + gh * kMSlotElems + lane * 8;
+    const float* bp = slotb + gh * kHeadState;
+    bf16x8 am[2][4][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
 #pragma unroll
       for (int d = 0; d < 4; ++d)
 #pragma unroll
         for (int hl = 0; hl < 2; ++hl)
-          P.a[d][hl] = *reinterpret_cast<const bf16x8*>(mp + ((w * 4 + d) * 2 + hl) * 512);
-      P.b = *reinterpret_cast<const f32x4*>(slotb + slot(j) * kHeadState + roff);
-    };
-    auto step = [&](int j, const ScanStep& P) {
-      // B fragments: slot s of chunk d is S[row][perm_depth(d, lg, s)]
-      f32x4 a0 = P.b, a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
+          am[e][d][hl] = *reinterpret_cast<const bf16x8*>(mp + (((2 * w + e) * 4 + d) * 2 + hl) * 512);
+    f32x4 acc[8][2];
+#pragma unroll
+    for (int vb = 0; vb < 8; ++vb)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        acc[vb][e] = *reinterpret_cast<const f32x4*>(bp + (16 * vb + l16) * kDim + 16 * (2 * w + e) + 4 * lg);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int vb = 0; vb < 8; ++vb) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const f32x4 x0 = *reinterpret_cast<const f32x4*>(&sx[l16][32 * d + 4 * lg]);
-        const f32x4 x1 = *reinterpret_cast<const f32x4*>(&sx[l16][32 * d + 16 + 4 * lg]);
+        // B fragment: slot s of chunk d is S[16 vb + l16][perm_depth(d, lg, s)]
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(&sm.s[16 * vb + l16][32 * d + 4 * lg]);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(&sm.s[16 * vb + l16][32 * d + 16 + 4 * lg]);
         const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
         bf16x8 sh, sl;
         split_frag(x, sh, sl);
-        a0 = mfma16(P.a[d][0], sh, a0);
-        a1 = mfma16(P.a[d][0], sl, a1);
-        a2 = mfma16(P.a[d][1], sh, a2);
-      }
-      const f32x4 acc = a0 + (a1 + a2);
-      __syncthreads();   // every wave has read S_j
-      *reinterpret_cast<f32x4*>(&sx[l16][16 * w + 4 * lg]) = acc;
-      if (j + 1 < nseg) {
-        *reinterpret_cast<f32x4*>(slotb + slot(j) * kHeadState + roff) = acc;
-        store_corr_frag(slotf + slot(j) * kFSlotElems, vt, w, lane, acc);
-      } else {
-        *reinterpret_cast<f32x4*>(new_state + (static_cast<size_t>(me.x) * kVHeads + h) * kHeadState + roff) = acc;
-      }
-      __syncthreads();   // S_{j+1} complete
-    };
-    ScanStep P0, P1, P2;
-    load(1, P0);
-    load(2, P1);
-    load(3, P2);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
-    for (int j = 1; j < nseg; j += 3) {
-      step(j, P0);
-      load(j + 3, P0);
-      __builtin_amdgcn_sched_barrier(0);
-      if (j + 1 < nseg) {
-        step(j + 1, P1);
-        load(j + 4, P1);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (j + 2 < nseg) {
-        step(j + 2, P2);
-        load(j + 5, P2);
-        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          acc[vb][e] = mfma16(am[e][d][0], sh, acc[vb][e]);
+          acc[vb][e] = mfma16(am[e][d][0], sl, acc[vb][e]);
+          acc[vb][e] = mfma16(am[e][d][1], sh, acc[vb][e]);
+        }
       }
     }
+    __syncthreads();   // every wave has read S_i
+    // acc[vb][e][rr] = S_{i+1}[16 vb + l16][16 (2w + e) + 4 lg + rr]
+#pragma unroll
+    for (int vb = 0; vb < 8; ++vb)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        *reinterpret_cast<f32x4*>(&sm.s[16 * vb + l16][16 * (2 * w + e) + 4 * lg]) = acc[vb][e];
+    __syncthreads();
   }
 }
 
-// ============================================================================
-// output correction: O = O0 + OI S_j^T for the chunks of segments >= 1
-// ============================================================================
-// One work-group per (chunk of a segment >= 1, v-head).  The state before the
-// segment, as the bf16 A fragments the scan wrote (32 KB), is copied straight
-// into LDS; wave w forms the 16 tokens 16 w .. 16 w + 15 for all 128 value
-// rows: D[v][t] = sum_k' S[v][k'] OI[t][k'], then out = bf16(O0 + D).  S
-// enters as a single bf16, as it does in Q S^T of the chunk recurrence.  The
-// wave's OI and O0 loads are issued with the copies; rows past the chunk end
-// fall outside the buffer resources (loads read 0, stores dropped).  Chunks
-// past the point where the segment's M-run stopped (its map bound below
-// kNegligibleLog2) keep out = O0.
-constexpr int kCorrThreads = 256;
-
-__global__ __launch_bounds__(kCorrThreads) void correct_kernel(int* __restrict__ lists, int num_seqs, int gcap,
-                                                               const int* __restrict__ mval,
-                                                               const uint16_t* __restrict__ slotf,
-                                                               const uint16_t* __restrict__ oi,
-                                                               uint16_t* __restrict__ out) {
-  __shared__ u32x4 sfrag[8][4][64];   // [v-tile][d][lane]
+__global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ lists, int num_seqs, int gcap,
+                                                             const float* __restrict__ slotb,
+                                                             const uint16_t* __restrict__ slotm,
+                                                             const int* __restrict__ mval,
+                                                             const uint16_t* __restrict__ oi,
+                                                             uint16_t* __restrict__ out,
+                                                             float* __restrict__ new_state) {
+  __shared__ FinishLds sm;
   const ListView lv = list_view(lists, num_seqs, gcap);
-  const int nsegs = lv.hdr[4], L = lv.hdr[2];
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int nmulti = lv.hdr[3], nsegs = lv.hdr[4], L = lv.hdr[2];
+  const int per_seg = (L + kFinChunks - 1) / kFinChunks;   // blocks per segment
+  const int ncorr = nsegs * per_seg * kVHeads;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int l16 = lane & 15, lg = lane >> 4;
-  for (int item = blockIdx.x; item < nsegs * L * kVHeads; item += gridDim.x) {
-    const int h = item & 7, u = item >> 3;
-    const int4 sg = lv.segs[u / L];
-    const int ci = u % L;                         // chunk within the segment
-    if (ci * kChunk >= sg.z) continue;            // past a short last segment
-    if (ci >= mval[static_cast<size_t>(sg.w + 1) * kVHeads + h]) continue;   // OI negligible: out = O0
-    const long long c0 = (static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32)) +
-                         static_cast<long long>(ci) * kChunk;
-    const int c = min(kChunk, sg.z - ci * kChunk);
-    __syncthreads();   // the previous item's readers of sfrag are done
-    {
-      // 32 KB: 8 copies of 1 KB per wave
-      const char* fsrc = reinterpret_cast<const char*>(slotf + (static_cast<size_t>(sg.w) * kVHeads + h) * kFSlotElems);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int blk = 8 * w + i;
-        dma16(fsrc + blk * 1024 + lane * 16, reinterpret_cast<char*>(&sfrag[0][0][0]) + blk * 1024);
+  for (int item = blockIdx.x; item < ncorr + nmulti * kVHeads; item += gridDim.x) {
+    const int h = item & 7;
+    if (item >= ncorr) {
+      // new_state = S_nseg
+      const int4 me = lv.multi[(item - ncorr) >> 3];
+      __syncthreads();   // the previous item's readers of sm are done
+      state_before(sm, me.y, me.z, h, slotb, slotm, mval, w, lane);
+      float* dst = new_state + (static_cast<size_t>(me.x) * kVHeads + h) * kHeadState;
+      for (int e = tid; e < kDim * kDim / 4; e += kFinThreads) {
+        const int row = e >> 5, col = (e & 31) * 4;
+        *reinterpret_cast<f32x4*>(dst + row * kDim + col) = *reinterpret_cast<const f32x4*>(&sm.s[row][col]);
       }
+      continue;
     }
-    const size_t rowbase = (static_cast<size_t>(c0) * kVHeads + h) * kDim;
-    const uint32_t bytes = static_cast<uint32_t>(c) * (kVHeads * kDim * 2);
-    const __amdgpu_buffer_rsrc_t orc = buf_rsrc(out + rowbase, bytes);
-    const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
-    const uint32_t trow = static_cast<uint32_t>(16 * w + l16) * (kVHeads * kDim * 2);
-    bf16x8 b[4];
+    const int u = item >> 3;
+    const int4 sg = lv.segs[u / per_seg];
+    const int tok = sg.z & ((1 << 17) - 1), j = sg.z >> 17;
+    const int g0 = sg.w - (j - 1);
+    const int first = (u % per_seg) * kFinChunks;   // first chunk of the block within the segment
+    const int nchunks = (tok + kChunk - 1) / kChunk;
+    const int formed = mval[static_cast<size_t>(g0 + j) * kVHeads + h] & (kMNegligible - 1);
+    const int last = min(min(first + kFinChunks, nchunks), formed);   // chunks [first, last) need OI S^T
+    if (first >= last) continue;
+    __syncthreads();   // the previous item's readers of sm are done
+    state_before(sm, g0, j, h, slotb, slotm, mval, w, lane);
+    // S -> bf16 correction fragments (in place: read, barrier, write)
+    u32x4 fr[2][4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-      b[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
-    u32x2 o0[8];
+    for (int e = 0; e < 2; ++e)
 #pragma unroll
-    for (int vt = 0; vt < 8; ++vt) o0[vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();   // waits for every load of the group, the copies into LDS included
+      for (int d = 0; d < 4; ++d) {
+        const float* sp = &sm.s[16 * (2 * w + e) + l16][32 * d + 8 * lg];
+        const f32x4 x0 = *reinterpret_cast<const f32x4*>(sp);
+        const f32x4 x1 = *reinterpret_cast<const f32x4*>(sp + 4);
+        fr[e][d] = u32x4{pack_bf2(x0[0], x0[1]), pack_bf2(x0[2], x0[3]), pack_bf2(x1[0], x1[1]),
+                         pack_bf2(x1[2], x1[3])};
+      }
+    __syncthreads();
 #pragma unroll
-    for (int vh = 0; vh < 2; ++vh) {
-      // four independent accumulators (value tiles 4 vh .. 4 vh + 3)
-      f32x4 acc[4];
+    for (int e = 0; e < 2; ++e)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int d = 0; d < 4; ++d) sm.frag[2 * w + e][d][lane] = fr[e][d];
+    __syncthreads();
+    const long long c0s = static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32);
+    for (int ci = first; ci < last; ++ci) {
+      // wave w: tokens 16 w .. 16 w + 15 of chunk ci, all 128 value rows
+      const long long c0 = c0s + static_cast<long long>(ci) * kChunk;
+      const int c = min(kChunk, tok - ci * kChunk);
+      const size_t rowbase = (static_cast<size_t>(c0) * kVHeads + h) * kDim;
+      const uint32_t bytes = static_cast<uint32_t>(c) * (kVHeads * kDim * 2);
+      const __amdgpu_buffer_rsrc_t orc = buf_rsrc(out + rowbase, bytes);
+      const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
+      const uint32_t trow = static_cast<uint32_t>(16 * w + l16) * (kVHeads * kDim * 2);
+      bf16x8 b[4];
 #pragma unroll
       for (int d = 0; d < 4; ++d)
+        b[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
+      u32x2 o0[8];
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          acc[e] = mfma16(__builtin_bit_cast(bf16x8, sfrag[4 * vh + e][d][lane]), b[d], acc[e]);
+      for (int vt = 0; vt < 8; ++vt)
+        o0[vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int vt = 4 * vh + e;
-        const u32x2 o = o0[vt];
-        const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[e][0], bf_hi(o.x) + acc[e][1]),
-                          pack_bf2(bf_lo(o.y) + acc[e][2], bf_hi(o.y) + acc[e][3])};
-        __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
+      for (int vh = 0; vh < 2; ++vh) {
+        f32x4 acc[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[e] = mfma16(__builtin_bit_cast(bf16x8, sm.frag[4 * vh + e][d][lane]), b[d], acc[e]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int vt = 4 * vh + e;
+          const u32x2 o = o0[vt];
+          const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[e][0], bf_hi(o.x) + acc[e][1]),
+                            pack_bf2(bf_lo(o.y) + acc[e][2], bf_hi(o.y) + acc[e][3])};
+          __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
+        }
       }
     }
   }
@@ -1955,7 +1959,6 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   auto* recs = reinterpret_cast<int4*>(ws + L.rec_off);
   auto* slotb = reinterpret_cast<float*>(ws + L.slotb_off);
   auto* slotm = reinterpret_cast<uint16_t*>(ws + L.slotm_off);
-  auto* slotf = reinterpret_cast<uint16_t*>(ws + L.slotf_off);
   auto* oi = reinterpret_cast<uint16_t*>(ws + L.oi_off);
   auto* mval = reinterpret_cast<int*>(ws + L.mval_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
@@ -1986,12 +1989,9 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
       num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm, mval);
   // a second segment needs more than kMinSegChunks chunks in one sequence
   if (total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
-    const long long g_scan = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads * 8, 512);
-    scan_kernel<<<dim3(static_cast<unsigned>(g_scan)), dim3(kScanThreads), 0, st>>>(lists, num_seqs, gc, slotb,
-                                                                                     slotm, slotf, new_state);
-    const long long g_corr = std::min<long long>(R * kVHeads, 1024);
-    correct_kernel<<<dim3(static_cast<unsigned>(g_corr)), dim3(kCorrThreads), 0, st>>>(lists, num_seqs, gc, mval,
-                                                                                        slotf, oi, ob);
+    const long long g_fin = std::min<long long>(R * kVHeads, 1024);
+    finish_kernel<<<dim3(static_cast<unsigned>(g_fin)), dim3(kFinThreads), 0, st>>>(lists, num_seqs, gc, slotb, slotm,
+                                                                                     mval, oi, ob, new_state);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
