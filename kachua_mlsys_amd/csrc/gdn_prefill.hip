@@ -234,6 +234,22 @@ __device__ __forceinline__ float dppf0(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
 }
 
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dppf0r(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROWS, 0xf, false));
+}
+
+// Inclusive prefix sum over the 64 lanes (fp32), as wave_incl_sum.
+__device__ __forceinline__ float wave_incl_sumf(float x) {
+  x += dppf0<0x111>(x);
+  x += dppf0<0x112>(x);
+  x += dppf0<0x114>(x);
+  x += dppf0<0x118>(x);
+  x += dppf0r<0x142, 0xa>(x);
+  x += dppf0r<0x143, 0xc>(x);
+  return x;
+}
+
 __device__ __forceinline__ float wave_sumf(float x) {
   x += dppf0<0x111>(x);
   x += dppf0<0x112>(x);
@@ -633,7 +649,7 @@ struct __align__(16) PrepassSmem {
     uint16_t kq[2][kChunk][kDim];   // K, Q rows (bf16, chunk-swizzled)
     float tm[kGva][kChunk][kMRow];  // T = (I + N)^{-1} per v-head of the pair
   } u;
-  float nm[kGva][kChunk][kMRow];    // N = strict lower beta_t rho K K^T; upper blocks are scratch
+  float nm[kGva][kChunk][kMRow];    // N = strict lower beta_t rho K K^T (before it: the record search's scratch)
   float lgam[kGva][kChunk];         // Gam_t / ln 2 (log2 cumulative decay)
   float beta[kGva][kChunk];
   float kb2[kGva][kChunk];          // log2 max(1, |1 - beta_t |k_t|^2|)
@@ -660,40 +676,22 @@ __device__ __forceinline__ void block_store(float* Z, const f32x4& v, float sc, 
   for (int rr = 0; rr < 4; ++rr) Z[(4 * lg + rr) * kMRow + l16] = sc * v[rr];
 }
 
-// Record r of a batch of at most kFusedPlanSeqs sequences (one per thread),
-// found by the work-group itself (no plan launch): exclusive scan of
-// per-sequence chunk counts; the thread owning the sequence that contains r
-// publishes it.  Returns false when record r does not exist.  scratch: 32 ints.
-constexpr int kFusedPlanSeqs = kPrepassThreads;   // larger batches: a plan launch is cheaper
+// Batches of at most kFusedPlanSeqs sequences number their records inside the
+// prepass (no plan launch): thread s owns sequence s, and an exclusive scan of
+// the chunk counts gives each sequence's first record.
+constexpr int kFusedPlanSeqs = kPrepassThreads;
 static_assert(kPlanScratch <= kGva * kChunk * kMRow, "planner scratch must fit in N's space");
 
-__device__ bool find_record(int r, const void* __restrict__ cu, int is64, int num_seqs, long long T,
-                            int* scratch, long long& t0_out, int& c_out) {
-  // num_seqs <= kPrepassThreads: thread s owns sequence s (one read of its bounds)
-  const int tid = threadIdx.x;
-  long long t0 = 0, t1 = 0;
-  if (tid < num_seqs) seq_bounds(cu, is64, tid, T, t0, t1);
-  const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
-  if (tid == 0) scratch[0] = -1;
-  const int inc = block_scan<kPrepassThreads>(nch, scratch + 16);
-  const int base = inc - nch;
-  if (nch > 0 && r >= base && r < base + nch) {
-    const long long c0 = t0 + static_cast<long long>(r - base) * kChunk;
-    scratch[0] = static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0));
-    scratch[2] = static_cast<int>(c0 & 0xffffffffLL);
-    scratch[3] = static_cast<int>(c0 >> 32);
-  }
-  __syncthreads();
-  c_out = scratch[0];
-  if (c_out < 0) return false;
-  t0_out = static_cast<long long>(static_cast<unsigned>(scratch[2])) | (static_cast<long long>(scratch[3]) << 32);
-  return true;
-}
+// At most this many prepass work-groups (two per CU); the grid never needs a
+// third round: the first work-groups, dispatched first, take a second item.
+constexpr int kPrepassGroups = 2 * 256;
+constexpr int kPrepassMaxGrid = 2 * kPrepassGroups;
 
-// One work-group per (record, q/k head): the K / Q rows and both grams are
-// shared by the two v-heads of the GVA pair; gates, weighting, inverse and
-// packing run per v-head on waves 0-3 / 4-7.
-__global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
+// Items (record, q/k head), item i = 4 r + hq; work-group wg takes items
+// wg, wg + nwg, ...  For each item the K / Q rows and both grams are shared by
+// the two v-heads of the GVA pair; gates, weighting, inverse and packing run
+// per v-head on waves 0-3 / 4-7.
+__global__ __launch_bounds__(kPrepassThreads, 4) void prepass_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
@@ -701,28 +699,50 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     int gcap, int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
     uint16_t* __restrict__ ws_frag, float* __restrict__ ws_gam) {
   __shared__ PrepassSmem sm;
+  int* scratch = reinterpret_cast<int*>(&sm.nm[0][0][0]);   // N's space until the grams
+  if (fused_plan && blockIdx.x == 0) {
+    // work-group 0 plans the batch (lists for the consumer) while the others
+    // run the records
+    int total_recs;
+    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, scratch, total_recs);
+    return;
+  }
+  const int wg = static_cast<int>(blockIdx.x) - fused_plan;
+  const int nwg = static_cast<int>(gridDim.x) - fused_plan;
+  // records: small batches scan the chunk counts here (thread s owns sequence s)
+  long long st0 = 0, st1 = 0;
+  int sbase = 0, snch = 0, total;
+  if (fused_plan) {
+    if (static_cast<int>(threadIdx.x) < num_seqs) seq_bounds(cu, is64, threadIdx.x, T, st0, st1);
+    snch = static_cast<int>((st1 - st0 + kChunk - 1) / kChunk);
+    const int inc = block_scan<kPrepassThreads>(snch, scratch + 16);
+    sbase = inc - snch;
+    if (threadIdx.x == kPrepassThreads - 1) scratch[8] = inc;
+    __syncthreads();
+    total = min(scratch[8], R);
+  } else {
+    total = min(rec_start[num_seqs], R);
+  }
+  for (int item = wg; item < total * kQKHeads; item += nwg) {
+  const int r = item / kQKHeads;
+  const int hq = item % kQKHeads;
   int c;
   long long t0;
-  int r, hq;
+  __syncthreads();   // the previous item's readers of T, N, the gates and the scratch are done
   if (fused_plan) {
-    // work-group 0 plans the batch (lists for the consumer) while the others
-    // run the records; N's space holds the scratch
-    if (blockIdx.x == 0) {
-      int total_recs;
-      plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists,
-                                  reinterpret_cast<int*>(&sm.nm[0][0][0]), total_recs);
-      return;
+    if (snch > 0 && r >= sbase && r < sbase + snch) {
+      const long long c0 = st0 + static_cast<long long>(r - sbase) * kChunk;
+      scratch[0] = static_cast<int>(min(static_cast<long long>(kChunk), st1 - c0));
+      scratch[2] = static_cast<int>(c0 & 0xffffffffLL);
+      scratch[3] = static_cast<int>(c0 >> 32);
     }
-    r = (blockIdx.x - 1) / kQKHeads;
-    hq = (blockIdx.x - 1) % kQKHeads;
-    if (!find_record(r, cu, is64, num_seqs, T, reinterpret_cast<int*>(&sm.nm[0][0][0]), t0, c)) return;
+    __syncthreads();
+    c = scratch[0];
+    t0 = static_cast<long long>(static_cast<unsigned>(scratch[2])) | (static_cast<long long>(scratch[3]) << 32);
     __syncthreads();   // scratch read by every thread before N is written
   } else {
-    r = blockIdx.x / kQKHeads;
-    hq = blockIdx.x % kQKHeads;
     const int4 rec = recs[r];
-    c = rec.z;
-    if (c <= 0) return;
+    c = max(rec.z, 1);
     t0 = rec.y;
   }
   const int tid = threadIdx.x;
@@ -768,15 +788,10 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
     const float lgv = t < c ? fmaxf(log_decay(alog, a_t, dtb), -100.0f) * kLog2e : 0.0f;
     const float bet = t < c ? sigmoidf(b_t) : 0.0f;
-    float scan = lgv;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float o = __shfl_up(scan, off, 64);
-      if (lane >= off) scan += o;
-    }
+    const float scan = wave_incl_sumf(lgv);
     sm.lgam[hh][t] = scan;
     sm.beta[hh][t] = bet;
-    const float last = __shfl(scan, c - 1, 64);
+    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scan), c - 1));
     float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * kGamStride;
     gp[t] = t < c ? fast_exp2(scan) : 0.0f;
     gp[kChunk + t] = t < c ? fast_exp2(last - scan) : 0.0f;
@@ -827,8 +842,12 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
         for (int rr = 0; rr < 4; ++rr) {
           const int t = 16 * mi + 4 * lg + rr;
           sm.nm[e][t][i] = i < t ? bt[rr] * fast_exp2(gt[rr] - gi_) * akk[n][rr] : 0.0f;
-          // diagonal: |k_t|^2 (rows t >= c have beta = 0 and contribute 0)
-          if (i == t) sm.kb2[e][t] = __log2f(fmaxf(1.0f, fabsf(1.0f - bt[rr] * akk[n][rr])));
+        }
+        if (mi == ni) {   // diagonal tile: |k_t|^2 (rows t >= c have beta = 0 and contribute 0)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (l16 == 4 * lg + rr)
+              sm.kb2[e][i] = __log2f(fmaxf(1.0f, fabsf(1.0f - bt[rr] * akk[n][rr])));
         }
       }
       {
@@ -858,32 +877,28 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
   }
   __syncthreads();   // N complete; K / Q space becomes T
 
-  // the chunk's map bound: sum over tokens of log2 g_t + log2 max(1, |1 - beta_t |k_t|^2|)
-  if (wl == 0) {
-    const float lb = wave_sumf(sm.kb2[hh][lane]) + sm.lgam[hh][c - 1];
-    if (lane == 0) ws_gam[(static_cast<size_t>(r) * kVHeads + h) * kGamStride + kBoundAt] = lb;
-  }
-
   // ---- T = (I + N)^{-1} per v-head: diagonal 16x16 blocks by forward substitution ----
   float (*nmh)[kMRow] = sm.nm[hh];
   float (*tmh)[kMRow] = sm.u.tm[hh];
   if (lane < 16) {
     const int base = 16 * wl;
     const int j = lane;
+    // column j of T_ii, updated column-wise: once x[i] is final, every later
+    // row subtracts N[r][i] x[i] (the same terms in the same order as the
+    // row-wise recurrence, but with a dependency depth of 16 instead of 120)
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      float acc = (i == j) ? 1.0f : 0.0f;
+    for (int i = 0; i < 16; ++i) x[i] = (i == j) ? 1.0f : 0.0f;
 #pragma unroll
-      for (int m2 = 0; m2 < i; ++m2) acc = fmaf(-nmh[base + i][base + m2], x[m2], acc);
-      x[i] = acc;
-    }
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int r = i + 1; r < 16; ++r) x[r] = fmaf(-nmh[base + r][base + i], x[i], x[r]);
 #pragma unroll
     for (int i = 0; i < 16; ++i) tmh[base + i][base + j] = x[i];
   }
 
   // ---- off-diagonal blocks by distance on fp32 MFMA:
-  //      T_ij = -T_ii P,  P = sum_{m=j}^{i-1} N_im T_mj  (P staged in N's unused upper block (j, i))
+  //      T_ij = -T_ii P,  P = sum_{m=j}^{i-1} N_im T_mj
 #pragma unroll
   for (int dist = 1; dist < 4; ++dist) {
     __syncthreads();
@@ -898,10 +913,13 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
       f32x4 pacc = pu[0];
 #pragma unroll
       for (int u = 1; u < dist; ++u) pacc += pu[u];
-      float* scr = &nmh[16 * bj][16 * bi];
-      block_store(scr, pacc, 1.0f, l16, lg);
+      // T_ii P with P straight from its C registers: MFMA kc of the product
+      // pairs depth 4 lg + kc, which lane (lg, l16) holds as pacc[kc] =
+      // P[4 lg + kc][l16]; the A operand reads T_ii at the same depth
       f32x4 tv = {0.f, 0.f, 0.f, 0.f};
-      tv = block_prod(tv, &tmh[16 * bi][16 * bi], scr, l16, lg);
+      const float* tii = &tmh[16 * bi][16 * bi];
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) tv = mfma_f32(tii[l16 * kMRow + 4 * lg + kc], pacc[kc], tv);
       block_store(&tmh[16 * bi][16 * bj], tv, -1.0f, l16, lg);
     }
   }
@@ -926,6 +944,13 @@ __global__ __launch_bounds__(kPrepassThreads) void prepass_kernel(
     }
     *reinterpret_cast<u32x4*>(frag2[e] + qi * 8) =
         u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
+  }
+
+  // the chunk's map bound: sum over tokens of log2 g_t + log2 max(1, |1 - beta_t |k_t|^2|)
+  if (wl == 0) {
+    const float lb = wave_sumf(sm.kb2[hh][lane]) + sm.lgam[hh][c - 1];
+    if (lane == 0) ws_gam[(static_cast<size_t>(r) * kVHeads + h) * kGamStride + kBoundAt] = lb;
+  }
   }
 }
 
@@ -1726,7 +1751,7 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 // maps are not negligible.  Work items, one work-group each:
 //   (segment j >= 1, block of kFinChunks chunks, v-head): S_j, then out =
 //        bf16(O0 + OI S_j^T) for the block's chunks whose OI was formed (the
-//        rest keep O0);
+//        rest keep O0), wave w taking chunk w of the block;
 //   (multi-segment sequence, v-head): new_state = S_nseg.
 // A scan step forms D = M^T S^T on MFMA with M^T as the M-run stored it (bf16
 // hi / lo) and S split into hi / lo from LDS (three products, fp32
@@ -1856,6 +1881,34 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
     const int formed = mval[static_cast<size_t>(g0 + j) * kVHeads + h] & (kMNegligible - 1);
     const int last = min(min(first + kFinChunks, nchunks), formed);   // chunks [first, last) need OI S^T
     if (first >= last) continue;
+    // wave w corrects chunk first + w (all 64 tokens, all 128 value rows); its
+    // OI and O0 loads are issued before the state is formed
+    const long long c0s = static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32);
+    const int ci = first + w;
+    const bool active = ci < last;
+    bf16x8 b[4][4];   // [token tile][d]: OI rows as B fragments
+    u32x2 o0[4][8];   // [token tile][value tile]: O0, four value columns
+    __amdgpu_buffer_rsrc_t orc = buf_rsrc(out, 0);
+    if (active) {
+      const long long c0 = c0s + static_cast<long long>(ci) * kChunk;
+      const int c = min(kChunk, tok - ci * kChunk);
+      const size_t rowbase = (static_cast<size_t>(c0) * kVHeads + h) * kDim;
+      const uint32_t bytes = static_cast<uint32_t>(c) * (kVHeads * kDim * 2);
+      orc = buf_rsrc(out + rowbase, bytes);
+      const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const uint32_t trow = static_cast<uint32_t>(16 * tt + l16) * (kVHeads * kDim * 2);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+          b[tt][d] = __builtin_bit_cast(
+              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
+#pragma unroll
+        for (int vt = 0; vt < 8; ++vt)
+          o0[tt][vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();   // the previous item's readers of sm are done
     state_before(sm, g0, j, h, slotb, slotm, mval, w, lane);
     // S -> bf16 correction fragments (in place: read, barrier, write)
@@ -1876,40 +1929,25 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
 #pragma unroll
       for (int d = 0; d < 4; ++d) sm.frag[2 * w + e][d][lane] = fr[e][d];
     __syncthreads();
-    const long long c0s = static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32);
-    for (int ci = first; ci < last; ++ci) {
-      // wave w: tokens 16 w .. 16 w + 15 of chunk ci, all 128 value rows
-      const long long c0 = c0s + static_cast<long long>(ci) * kChunk;
-      const int c = min(kChunk, tok - ci * kChunk);
-      const size_t rowbase = (static_cast<size_t>(c0) * kVHeads + h) * kDim;
-      const uint32_t bytes = static_cast<uint32_t>(c) * (kVHeads * kDim * 2);
-      const __amdgpu_buffer_rsrc_t orc = buf_rsrc(out + rowbase, bytes);
-      const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
-      const uint32_t trow = static_cast<uint32_t>(16 * w + l16) * (kVHeads * kDim * 2);
-      bf16x8 b[4];
+    if (active) {
 #pragma unroll
-      for (int d = 0; d < 4; ++d)
-        b[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
-      u32x2 o0[8];
-#pragma unroll
-      for (int vt = 0; vt < 8; ++vt)
-        o0[vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
-#pragma unroll
-      for (int vh = 0; vh < 2; ++vh) {
+      for (int vt = 0; vt < 8; ++vt) {
+        // four independent accumulators (token tiles)
         f32x4 acc[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tt = 0; tt < 4; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < 4; ++d) {
+          const bf16x8 a_ = __builtin_bit_cast(bf16x8, sm.frag[vt][d][lane]);
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            acc[e] = mfma16(__builtin_bit_cast(bf16x8, sm.frag[4 * vh + e][d][lane]), b[d], acc[e]);
+          for (int tt = 0; tt < 4; ++tt) acc[tt] = mfma16(a_, b[tt][d], acc[tt]);
+        }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int vt = 4 * vh + e;
-          const u32x2 o = o0[vt];
-          const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[e][0], bf_hi(o.x) + acc[e][1]),
-                            pack_bf2(bf_lo(o.y) + acc[e][2], bf_hi(o.y) + acc[e][3])};
+        for (int tt = 0; tt < 4; ++tt) {
+          const u32x2 o = o0[tt][vt];
+          const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[tt][0], bf_hi(o.x) + acc[tt][1]),
+                            pack_bf2(bf_lo(o.y) + acc[tt][2], bf_hi(o.y) + acc[tt][3])};
+          const uint32_t trow = static_cast<uint32_t>(16 * tt + l16) * (kVHeads * kDim * 2);
           __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
         }
       }
@@ -1976,7 +2014,8 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (!fused_plan)
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                         total_tokens, Ri, gc, rec_start, recs, lists);
-  prepass_kernel<<<dim3(static_cast<unsigned>(R * kQKHeads + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
+  const long long g_pre = std::min<long long>(R * kQKHeads, kPrepassMaxGrid - fused_plan);
+  prepass_kernel<<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
       qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
       Ri, gc, fused_plan, rec_start, lists, frag, gam);
   // persistent grids: one work-group per CU per consumer kind at most; a
