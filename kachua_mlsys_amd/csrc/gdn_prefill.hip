@@ -636,6 +636,16 @@ __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
 }
 
+typedef __attribute__((ext_vector_type(4))) short i16x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// gfx950 transposed LDS read: in each 16-lane group, lane i receives element
+// (i & 3) of the 8-byte vectors addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
+__device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // ============================================================================
 // prepass: chunk-local WY terms for one (record, v-head)
 // ============================================================================
@@ -981,16 +991,6 @@ struct __align__(16) ConsumerSmem {
 };
 
 __device__ __forceinline__ int v_swz(int t) { return (t & 3) << 2; }
-
-typedef __attribute__((ext_vector_type(4))) short i16x4;
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-// gfx950 transposed LDS read: in each 16-lane group, lane i receives element
-// (i & 3) of the 8-byte vectors addressed by lanes i/4, i/4+4, i/4+8, i/4+12.
-__device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
-  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
-  return __builtin_bit_cast(u32x2, v);
-}
 
 __device__ __forceinline__ bf16x8 join_frag(u32x2 lo, u32x2 hi) {
   return __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
@@ -1410,34 +1410,58 @@ __device__ __forceinline__ void state_frags(const f32x4 (&st)[8], bf16x8 (&sb)[4
 }
 
 // Chain wave, one chunk: S^T tile st (kappa k order, as in consumer_chunk).
+// Each phase issues all of its LDS operand reads before its first product and
+// runs its products over independent accumulators, so neither the LDS latency
+// nor the MFMA result latency is paid per product.
 template <int P>
 __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8], int w, int lane) {
   const int l16 = lane & 15, lg = lane >> 4;
-  bf16x8 sb[4];
-  state_frags(st, sb);
-
-  // ---- X = K S^T ----
   const int rsw = kq_swz(l16);
-  f32x4 X[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-      X[m] = mfma16(*reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]),
-                    sb[d], X[m]);
-  }
-  // ---- R = V - gam X, Delta = Tb R (fp16) ----
   const int vrow = 4 * lg + (l16 >> 2);
   const int vat = 8 * ((2 * w + ((l16 & 3) >> 1)) ^ vh_swz(vrow)) + 4 * (l16 & 1);
+
+  // ---- operands of X = K S^T and R = V - gam X ----
+  bf16x8 ka[4][4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      ka[d][m] = *reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]);
+  f32x4 gam[4];
+  u32x2 vw[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    gam[m] = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
+    vw[m] = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
+  }
+  bf16x8 sb[4];
+  state_frags(st, sb);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- X = K S^T ----
+  f32x4 X[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[d][m], sb[d], X[m]);
+  // Tb fragments land while X runs
+  f16x8 tb[2][4];
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      tb[d][m] = *reinterpret_cast<const f16x8*>(&sm.frag[P][0][((m * 2 + d) * 64 + lane) * 8]);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- R = V - gam X, Delta = Tb R (fp16) ----
   f32x4 Rt[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    const f32x4 gam = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
-    const u32x2 vw = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
-    const float vv[4] = {bf_lo(vw.x), bf_hi(vw.x), bf_lo(vw.y), bf_hi(vw.y)};
+    const float vv[4] = {bf_lo(vw[m].x), bf_hi(vw[m].x), bf_lo(vw[m].y), bf_hi(vw[m].y)};
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[rr] * X[m][rr];
+    for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[m][rr] * X[m][rr];
   }
   f16x8 rf[2];
 #pragma unroll
@@ -1448,12 +1472,33 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   }
   f32x4 D[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < 4; ++m) D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 2; ++d)
-      D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][((m * 2 + d) * 64 + lane) * 8]), rf[d], D[m]);
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) D[m] = mfma16h(tb[d][m], rf[d], D[m]);
+
+  // operands of the state update, read while Delta forms: tail gates and the
+  // K^T fragments (tile kt, row i of the A operand is k = kappa(kt, i/4, i%4);
+  // lane sl of group lg addresses K[t][k0 .. k0+3], t = perm_depth(d, lg, sl/4)
+  // (+16 for slots 4..7), k0 = 32 (kt >> 1) + 8 (sl & 3) + 4 (kt & 1))
+  f32x4 tl[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) tl[m] = *reinterpret_cast<const f32x4*>(&sm.gt[P][kChunk + 16 * m + 4 * lg]);
+  const float gam_c = sm.gt[P][c - 1];
+  const int sl = l16;
+  const int tsw = kq_swz(4 * lg + (sl >> 2));
+  bf16x8 kta[2][8];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) {
+    const int ta = perm_depth(d, lg, sl >> 2);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      const int at = 8 * ((4 * (kt >> 1) + (sl & 3)) ^ tsw) + 4 * (kt & 1);
+      kta[d][kt] = join_frag(lds_tr16(&sm.ks[P][ta][at]), lds_tr16(&sm.ks[P][ta + 16][at]));
+    }
   }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
     float x[8];
@@ -1467,7 +1512,7 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   {
     f32x4 Dt[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) Dt[m] = D[m] * *reinterpret_cast<const f32x4*>(&sm.gt[P][kChunk + 16 * m + 4 * lg]);
+    for (int m = 0; m < 4; ++m) Dt[m] = D[m] * tl[m];
 #pragma unroll
     for (int d = 0; d < 2; ++d) {
       float x[8];
@@ -1475,24 +1520,14 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
       split_frag(x, dh[d], dl[d]);
     }
   }
-  const float gam_c = sm.gt[P][c - 1];
-  // K^T fragments: tile kt, row i of the A operand is k = kappa(kt, i/4, i%4);
-  // lane sl of group lg addresses K[t][k0 .. k0+3], t = perm_depth(d, lg, sl/4)
-  // (+16 for slots 4..7), k0 = 32 (kt >> 1) + 8 (sl & 3) + 4 (kt & 1).
-  const int sl = l16;
-  const int tsw = kq_swz(4 * lg + (sl >> 2));
 #pragma unroll
-  for (int kt = 0; kt < 8; ++kt) {
-    f32x4 acc = st[kt] * gam_c;
-    const int at = 8 * ((4 * (kt >> 1) + (sl & 3)) ^ tsw) + 4 * (kt & 1);
+  for (int kt = 0; kt < 8; ++kt) st[kt] = st[kt] * gam_c;
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      const int ta = perm_depth(d, lg, sl >> 2);
-      const bf16x8 kta = join_frag(lds_tr16(&sm.ks[P][ta][at]), lds_tr16(&sm.ks[P][ta + 16][at]));
-      acc = mfma16(kta, dh[d], acc);
-      acc = mfma16(kta, dl[d], acc);
-    }
-    st[kt] = acc;
+  for (int d = 0; d < 2; ++d) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = mfma16(kta[d][kt], dh[d], st[kt]);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = mfma16(kta[d][kt], dl[d], st[kt]);
   }
   // S fragments of the next chunk for the side wave (read before its next B2)
   bf16x8 nb[4];
@@ -1510,32 +1545,49 @@ __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, floa
   // while the chain wave is in its VALU-heavy R / Delta phase instead of X
   copy_next();
   const int rsw = kq_swz(l16);
-  bf16x8 sb[4];
+  bf16x8 sb[4], qa[4][4];
 #pragma unroll
-  for (int d = 0; d < 4; ++d) sb[d] = __builtin_bit_cast(bf16x8, sm.sbx[ws][d][lane]);
+  for (int d = 0; d < 4; ++d) {
+    sb[d] = __builtin_bit_cast(bf16x8, sm.sbx[ws][d][lane]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      qa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 YT[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int m = 0; m < 4; ++m) YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-      YT[m] = mfma16(sb[d], *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]),
-                     YT[m]);
+  for (int d = 0; d < 4; ++d)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) YT[m] = mfma16(sb[d], qa[d][m], YT[m]);
+  // Aqk fragments and gates of the output phase
+  bf16x8 fa[2][4];
+  float sg[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d)
+      fa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][((m * 2 + d) * 64 + lane) * 8]);
+    sg[m] = scale * sm.gt[P][16 * m + l16];
   }
   lds_barrier();   // B2
   bf16x8 dob[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) dob[d] = __builtin_bit_cast(bf16x8, sm.dox[ws][d][lane]);
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 OT[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) OT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int d = 0; d < 2; ++d)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) OT[m] = mfma16(dob[d], fa[d][m], OT[m]);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
-    f32x4 OT = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 2; ++d)
-      OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][((m * 2 + d) * 64 + lane) * 8]), OT);
     const int t = 16 * m + l16;
-    const float sg = scale * sm.gt[P][t];
-    const u32x2 pk = {pack_bf2(sg * YT[m][0] + scale * OT[0], sg * YT[m][1] + scale * OT[1]),
-                      pack_bf2(sg * YT[m][2] + scale * OT[2], sg * YT[m][3] + scale * OT[3])};
+    const u32x2 pk = {pack_bf2(sg[m] * YT[m][0] + scale * OT[m][0], sg[m] * YT[m][1] + scale * OT[m][1]),
+                      pack_bf2(sg[m] * YT[m][2] + scale * OT[m][2], sg[m] * YT[m][3] + scale * OT[m][3])};
     __builtin_amdgcn_raw_buffer_store_b64(pk, orc, static_cast<uint32_t>(t) * (kVHeads * kDim * 2) + ocol, 0, 0);
   }
 }
@@ -1672,7 +1724,7 @@ __device__ __forceinline__ void split_items(
   }
   if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed | (formed < n ? kMNegligible : 0);
 
-  if (chain) {
+  if (chain && !(mrun && formed < n)) {   // a stopped M-run's map is negligible: never read
     if (slot < 0 || !mrun) {
       float* dst = slot < 0 ? new_state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState
                             : slotb + (static_cast<size_t>(slot) * kVHeads + h) * kHeadState;
@@ -1704,7 +1756,7 @@ __device__ __forceinline__ void split_items(
   }
   claim();
   if (threadIdx.x == 0) sm.next_item = claimed;
-  __syncthreads();
+  lds_barrier();   // publishes the next item; the item's stores stay in flight
   item = sm.next_item;
   }
 }
