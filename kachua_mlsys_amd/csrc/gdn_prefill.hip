@@ -625,10 +625,16 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, const f32x4& c) {
 }
 
 // K / Q rows in LDS keep natural column order; the 16-byte chunk j of row t is
-// stored at position j ^ kq_swz(t).  kq_swz is a bijection of t & 15, so the
-// row reads (8 consecutive k of 16 rows) and the transposed reads (4
-// consecutive k of 4 rows x 4 chunks) are bank-conflict free.
-__device__ __forceinline__ int kq_swz(int t) { return ((t & 3) << 2) | ((t >> 2) & 3); }
+// stored at position j ^ kq_swz(t).  kq_swz is linear over GF(2) in t & 15:
+// bits 0-1 of t move to bits 2-3, bit 2 adds 2 and bit 3 adds 3.  Chosen by
+// measurement on gfx950 (64 banks) among all linear maps: the row reads (8
+// consecutive k of 16 rows, ds_read_b128) run conflict-free and the transposed
+// reads (4 consecutive k of 4 rows x 4 chunks, ds_read_b64_tr_b16) at their
+// floor of two passes per 32 lanes; the earlier map
+// ((t & 3) << 2) | ((t >> 2) & 3) took twice as long for the row reads.
+__device__ __forceinline__ int kq_swz(int t) {
+  return ((t & 3) << 2) | ((((t >> 2) & 1) << 1) ^ (((t >> 3) & 1) * 3));
+}
 
 // 16 bytes per lane from global memory straight into LDS: lane i of the wave
 // writes bytes [16 i, 16 i + 16) after the wave-uniform LDS address.
@@ -974,9 +980,8 @@ constexpr int kConsumerThreads = 64 * kConsumerWaves;
 // of every field (not of a struct of fields) so that buffer 1 of a field sits
 // within a ds_read immediate offset of buffer 0.
 //   ks / qs : K / Q rows in natural column order; the 16-byte chunk j of row t
-//             is stored at position j ^ kq_swz(t), which makes the row reads
-//             (8 consecutive k) and the transposed reads (4 consecutive k of 4
-//             rows) bank-conflict free.
+//             is stored at position j ^ kq_swz(t) (row reads conflict-free,
+//             transposed reads at two passes per 32 lanes).
 //   vs      : V rows; chunk j of row t at j ^ v_swz(t).
 //   frag    : Tb (fp16), Aqk (bf16) in permuted fragment order (lane-contiguous).
 //   gt      : gam[64], tail[64] and 128 floats of padding.
