@@ -42,6 +42,7 @@
 // bf16.  The fp32 state never leaves registers between chunks.
 #include "gdn_common.h"
 #include <algorithm>
+#include <type_traits>
 #include "../../include/gdn_mi355x.h"
 
 namespace gdn {
@@ -111,6 +112,9 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 //                 final-state slot or -1 for new_state, first record)
 //   runs[2i+1] = (first token lo, hi, chunks with records, chunks)
 //   flags: kRunM (M-run), kRunFromState (initial state from `state`)
+//   shorts[i]  = (seq, record of its chunk or -1 when it has none, first token
+//                 lo, first token hi | tokens << 16) for sequences of at most
+//                 one chunk
 constexpr int kListHdr = 16;
 constexpr int kRunM = 1;
 constexpr int kRunFromState = 2;
@@ -121,7 +125,7 @@ struct ListView {
   int4* multi;
   int4* segs;
   int4* runs;
-  int* shorts;
+  int4* shorts;
 };
 
 __host__ __device__ inline ListView list_view(int* lists, int num_seqs, long long gcap) {
@@ -130,13 +134,13 @@ __host__ __device__ inline ListView list_view(int* lists, int num_seqs, long lon
   v.multi = reinterpret_cast<int4*>(lists + kListHdr);
   v.segs = v.multi + num_seqs;
   v.runs = v.segs + gcap;
-  v.shorts = reinterpret_cast<int*>(v.runs + 2 * max_runs(num_seqs, gcap));
+  v.shorts = v.runs + 2 * max_runs(num_seqs, gcap);
   return v;
 }
 
 __host__ __device__ inline size_t list_ints(int num_seqs, long long gcap) {
   return kListHdr + 4 * static_cast<size_t>(num_seqs) + 4 * static_cast<size_t>(gcap) +
-         8 * static_cast<size_t>(max_runs(num_seqs, gcap)) + static_cast<size_t>(num_seqs);
+         8 * static_cast<size_t>(max_runs(num_seqs, gcap)) + 4 * static_cast<size_t>(num_seqs);
 }
 
 // ---- workspace layout -------------------------------------------------------
@@ -537,7 +541,10 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     rec_start[s] = rb;
     rb += nch;
     if (!p.is_long) {
-      lv.shorts[sp++] = s;
+      // chunks whose records exist (overlapping cu_seqlens can exhaust the capacity)
+      const int rec = nch > 0 && rec0 < R ? rec0 : -1;
+      lv.shorts[sp++] = make_int4(s, rec, static_cast<int>(t0 & 0xffffffffLL),
+                                  static_cast<int>(t0 >> 32) | (static_cast<int>(t1 - t0) << 16));
       continue;
     }
     const int g0 = p.multi ? gb : 0;
@@ -650,6 +657,15 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 __device__ __forceinline__ u32x2 lds_tr16(const uint16_t* p) {
   const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
   return __builtin_bit_cast(u32x2, v);
+}
+
+// Work-group barrier that waits for this wave's LDS operations only; its
+// global-to-LDS copies stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt / expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // ============================================================================
@@ -1205,56 +1221,48 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
   }
 }
 
-// Full-head consumer over the short-sequence list: work item = (list entry,
-// v-head), item i on work-group wg = i mod nwg.  nwg and the work-group's
-// linear id are multiples of 8 apart, so v-head h runs on XCD h (XCD = linear
-// id % 8), where its prepass records were written.
+// Full-head consumer over the short-sequence list (sequences of at most one
+// chunk): work item = (list entry, v-head), item i on work-group wg = i mod
+// nwg.  nwg and the work-group's linear id are multiples of 8 apart, so v-head
+// h runs on XCD h (XCD = linear id % 8), where its prepass records were
+// written.  Items are software-pipelined so that the state and operand traffic
+// of one item overlaps the compute of the previous one: item k computes from
+// LDS buffer k & 1 and its state registers while item k+1's state loads and
+// operand copies (into the other buffer) are in flight and item k+2's list
+// entry is loaded.  Every wave's vector-memory operations retire in issue
+// order, so at the start of item k's stage, "at most 9 outstanding" (the list
+// entry of item k+1 and the 8 new_state stores of item k-1, all issued after
+// item k's loads) means item k's state and copies have landed.
+struct ShortItem {
+  int s, h, rec, c;   // sequence, v-head, record (-1: no chunk), tokens
+  long long c0;
+};
+
+// The list entry arrives in VGPRs (see entry() below) and becomes scalar here.
+__device__ __forceinline__ ShortItem short_item(const int4& e, int item) {
+  ShortItem it;
+  it.s = __builtin_amdgcn_readfirstlane(e.x);
+  it.h = item & 7;
+  it.rec = __builtin_amdgcn_readfirstlane(e.y);
+  const int zw = __builtin_amdgcn_readfirstlane(e.w);
+  it.c = zw >> 16;
+  it.c0 = static_cast<long long>(static_cast<unsigned>(__builtin_amdgcn_readfirstlane(e.z))) |
+          (static_cast<long long>(zw & 0xffff) << 32);
+  return it;
+}
+
 __device__ __forceinline__ void full_head_items(
-    ConsumerSmem& sm, int wg, int nwg, const int* __restrict__ list, int nseq,
+    ConsumerSmem& sm, int wg, int nwg, const int4* __restrict__ list, int nseq,
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
-    const float* __restrict__ state, const void* __restrict__ cu, int is64, long long T, int R, float scale,
-    const int* __restrict__ rec_start, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
-    uint16_t* __restrict__ out, float* __restrict__ new_state) {
-  for (int item = wg; item < nseq * kVHeads; item += nwg) {
-  const int h = item & 7;
-  const int s = list[item >> 3];
-  const int hq = h / kGva;
+    const float* __restrict__ state, float scale, const uint16_t* __restrict__ ws_frag,
+    const float* __restrict__ ws_gam, uint16_t* __restrict__ out, float* __restrict__ new_state) {
+  const int nitems = nseq * kVHeads;
+  if (wg >= nitems) return;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int l16 = lane & 15, lg = lane >> 4;
   const int vcol = 16 * w;                       // first value row of this wave's tile
-
-  long long t0, t1;
-  seq_bounds(cu, is64, s, T, t0, t1);
-  // state tile in the kappa k order (see consumer_chunk)
-  const size_t st_off = ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim + 8 * lg;
-  auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
-  if (t1 <= t0) {   // empty sequence: the reference leaves new_state zero
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt)
-      *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = f32x4{0.f, 0.f, 0.f, 0.f};
-    continue;
-  }
-  const int rec0 = rec_start[s];
-  const long long nchunks = (t1 - t0 + kChunk - 1) / kChunk;
-  // chunks whose records exist (overlapping cu_seqlens can exhaust the capacity)
-  const long long nvalid = rec0 >= R ? 0 : min(nchunks, static_cast<long long>(R - rec0));
-  auto chunk_ref = [&](long long idx) {
-    const long long c0 = t0 + idx * kChunk;
-    return ChunkRef{c0, static_cast<int>(min(static_cast<long long>(kChunk), t1 - c0)),
-                    rec0 + static_cast<int>(idx)};
-  };
-
-  f32x4 st[8];
-  if (state != nullptr) {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(state + st_off + kappa0(kt));
-  } else {
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-
   DmaLane dl;
   {
     const int r = 4 * w + (lane >> 4);     // + 32 j keeps r & 15
@@ -1263,35 +1271,72 @@ __device__ __forceinline__ void full_head_items(
     dl.v_col = 16u * static_cast<uint32_t>((lane & 15) ^ v_swz(r));
   }
   const uint32_t ocol = 2u * static_cast<uint32_t>(vcol + 4 * lg);
-  auto out_rsrc = [&](const ChunkRef& cr) {
-    return __builtin_amdgcn_make_buffer_rsrc(out + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim, 0,
-                                             cr.c * (kVHeads * kDim * 2), 0x00020000);
+  auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
+  // state tile in the kappa k order (see consumer_chunk)
+  auto st_off = [&](const ShortItem& it) {
+    return ((static_cast<size_t>(it.s) * kVHeads + it.h) * kDim + vcol + l16) * kDim + 8 * lg;
   };
-
-  if (nvalid > 0) {
-    // Chunk i computes from buffer i & 1 while the copies of chunk i+1 into the
-    // other buffer are in flight; the barrier closing chunk i waits for them
-    // (and frees buffer i & 1 for chunk i+2).
-    dma_chunk<0>(sm, chunk_ref(0), dl, w, lane, h, hq, q, k, v, ws_frag, ws_gam);
-    __syncthreads();
-    for (long long i = 0; i < nvalid; i += 2) {
-      {
-        if (i + 1 < nvalid) dma_chunk<1>(sm, chunk_ref(i + 1), dl, w, lane, h, hq, q, k, v, ws_frag, ws_gam);
-        const ChunkRef cr = chunk_ref(i);
-        consumer_chunk<0>(sm, cr.c, st, w, lane, scale, out_rsrc(cr), ocol);
-        __syncthreads();
-      }
-      if (i + 1 < nvalid) {
-        if (i + 2 < nvalid) dma_chunk<0>(sm, chunk_ref(i + 2), dl, w, lane, h, hq, q, k, v, ws_frag, ws_gam);
-        const ChunkRef cr = chunk_ref(i + 1);
-        consumer_chunk<1>(sm, cr.c, st, w, lane, scale, out_rsrc(cr), ocol);
-        __syncthreads();
-      }
-    }
-  }
-
+  auto load_state = [&](const ShortItem& it, f32x4 (&st)[8]) {
+    if (state != nullptr && it.c > 0) {
+      const float* sp = state + st_off(it);
 #pragma unroll
-  for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(new_state + st_off + kappa0(kt)) = st[kt];
+      for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(sp + kappa0(kt));
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto issue = [&](const ShortItem& it, f32x4 (&st)[8], auto PC) {
+    constexpr int P = decltype(PC)::value;
+    load_state(it, st);
+    if (it.rec >= 0 && it.c > 0)
+      dma_chunk<P>(sm, ChunkRef{it.c0, it.c, it.rec}, dl, w, lane, it.h, it.h / kGva, q, k, v, ws_frag, ws_gam);
+  };
+  // the list entry of item i (a valid entry past the end keeps one load per
+  // stage).  An opaque zero makes the address lane-varying, so the entry stays
+  // in VGPRs until short_item() reads it one stage later: waiting for it then
+  // does not wait for the loads and copies issued after it.
+  int zero_v;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero_v));
+  auto entry = [&](int i) { return list[((i < nitems ? i : 0) >> 3) + zero_v]; };
+
+  int item = wg;
+  ShortItem cur = short_item(entry(item), item);
+  f32x4 st[8];
+  issue(cur, st, std::integral_constant<int, 0>{});
+  int4 enext = entry(item + nwg);
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // one item from buffer P; returns false after the group's last item
+  auto stage = [&](auto PC) -> bool {
+    constexpr int P = decltype(PC)::value;
+    __builtin_amdgcn_s_waitcnt(0x0f79);   // vmcnt(9): this item's state and copies have landed
+    lds_barrier();                         // ... in every wave
+    const int inext = item + nwg;
+    const bool has_next = inext < nitems;
+    const ShortItem nx = short_item(enext, inext);
+    f32x4 stn[8];
+    if (has_next) issue(nx, stn, std::integral_constant<int, P ^ 1>{});
+    enext = entry(inext + nwg);
+    if (cur.rec >= 0 && cur.c > 0) {
+      const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
+          out + (static_cast<size_t>(cur.c0) * kVHeads + cur.h) * kDim, 0, cur.c * (kVHeads * kDim * 2), 0x00020000);
+      consumer_chunk<P>(sm, cur.c, st, w, lane, scale, orc, ocol);
+    }
+    // an empty sequence leaves new_state zero (st is zero); a chunk without a
+    // record (malformed cu_seqlens) passes the state through
+    float* dst = new_state + st_off(cur);
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(dst + kappa0(kt)) = st[kt];
+    lds_barrier();   // buffer P is free for item k+2's copies
+    if (!has_next) return false;
+    item = inext;
+    cur = nx;
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = stn[kt];
+    return true;
+  };
+  while (stage(std::integral_constant<int, 0>{}) && stage(std::integral_constant<int, 1>{})) {
   }
 }
 
@@ -1325,15 +1370,6 @@ struct __align__(16) SplitSmem {
 };
 
 __device__ __forceinline__ int vh_swz(int t) { return ((t >> 1) & 1) << 2; }
-
-// Work-group barrier that waits for this wave's LDS operations only; its
-// global-to-LDS copies stay in flight.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt / expcnt unconstrained
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
 
 // Buffer resource over [base, base + bytes): loads past the end return zeros
 // and stores past it are dropped by the hardware range check.
@@ -1794,7 +1830,7 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
     __builtin_amdgcn_s_waitcnt(0);
   } else {
     full_head_items(sm.full, bid - g_long, static_cast<int>(gridDim.x) - g_long, lv.shorts, lv.hdr[1],
-                    q, k, v, state, cu, is64, T, R, scale, rec_start, ws_frag, ws_gam, out, new_state);
+                    q, k, v, state, scale, ws_frag, ws_gam, out, new_state);
   }
 }
 
