@@ -13,7 +13,7 @@
 // one (n, h) tile.  Lane l = 32*half + lam reads columns [4 lam, 4 lam + 4) of
 // rows v0 + half*ROWS/2 + i, i < ROWS/2, with one 16-byte load per row, so every
 // load instruction of the wave covers two whole 512-byte rows.  Each state byte
-// is read once and written once (non-temporal store).  The 2*ROWS/2 row dots
+// is read once and written once (non-temporal loads and stores).  The 2*ROWS/2 row dots
 // (S k and S q for each row) are reduced over the 32 lanes of each half with a
 // reduce-scatter butterfly (DPP / ds_swizzle), which leaves exactly one fully
 // reduced value per lane; delta is then broadcast to the half through LDS.
@@ -58,10 +58,13 @@ __global__ __launch_bounds__(64) void decode_kernel(
   const int row0 = vt * ROWS + half * NL;
 
   // ---- issue the state loads first (the only large traffic) ----
+  // Non-temporal: every state byte is read exactly once, so the loads stream
+  // instead of allocating in L2 / MALL (measured on MI355X at B = 64: 11.84 ->
+  // 10.84 us per step with plain vs non-temporal loads, same outputs).
   const float* src = state + static_cast<size_t>(nh) * kHeadState + row0 * kDim + lam * 4;
   f32x4 s[NL];
 #pragma unroll
-  for (int i = 0; i < NL; ++i) s[i] = *reinterpret_cast<const f32x4*>(src + i * kDim);
+  for (int i = 0; i < NL; ++i) s[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + i * kDim));
 
   // ---- q, k for this lane's 4 columns; gates for this (n, h) ----
   const size_t qk_off = (static_cast<size_t>(n) * kQKHeads + hq) * kDim + lam * 4;
