@@ -1280,7 +1280,7 @@ __device__ __forceinline__ void full_head_items(
     if (state != nullptr && it.c > 0) {
       const float* sp = state + st_off(it);
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(sp + kappa0(kt));
+      for (int kt = 0; kt < 8; ++kt) st[kt] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sp + kappa0(kt)));
     } else {
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1324,10 +1324,11 @@ __device__ __forceinline__ void full_head_items(
       consumer_chunk<P>(sm, cur.c, st, w, lane, scale, orc, ocol);
     }
     // an empty sequence leaves new_state zero (st is zero); a chunk without a
-    // record (malformed cu_seqlens) passes the state through
+    // record (malformed cu_seqlens) passes the state through.  State bytes are
+    // read and written once: non-temporal, as in decode.
     float* dst = new_state + st_off(cur);
 #pragma unroll
-    for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(dst + kappa0(kt)) = st[kt];
+    for (int kt = 0; kt < 8; ++kt) __builtin_nontemporal_store(st[kt], reinterpret_cast<f32x4*>(dst + kappa0(kt)));
     lds_barrier();   // buffer P is free for item k+2's copies
     if (!has_next) return false;
     item = inext;
