@@ -1380,9 +1380,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uin
 
 // 16 bytes per lane through a buffer resource straight into LDS (lane i of the
 // wave writes bytes [16 i, 16 i + 16) after the wave-uniform LDS address).
+// AUX is the cache policy of the load: 2 (nt) streams data read exactly once.
+template <int AUX = 0>
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rs, uint32_t voff, void* lds_wave_base) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds_wave_base, 16,
-                                           voff, 0, 0, 0);
+                                           voff, 0, 0, AUX);
 }
 
 // Per-lane byte offsets of the side-wave copies; chunk-invariant because each
@@ -1431,7 +1433,7 @@ __device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, con
   const __amdgpu_buffer_rsrc_t vr = buf_rsrc(v + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
                                              zero_v ? 0u : static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
 #pragma unroll
-  for (int j = 0; j < 2; ++j) dma16_buf(vr, dl.v[j], &sm.vs[P][32 * j + 8 * ws][0]);
+  for (int j = 0; j < 2; ++j) dma16_buf<2>(vr, dl.v[j], &sm.vs[P][32 * j + 8 * ws][0]);   // V: read once
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
   const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kFrags * kFragElems, kFrags * kFragElems * 2);
 #pragma unroll
@@ -1700,7 +1702,7 @@ __device__ __forceinline__ void split_items(
     } else if (from_state && state != nullptr) {
       const float* sp = state + ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim;
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) st[kt] = *reinterpret_cast<const f32x4*>(sp + kappa(kt, 0));
+      for (int kt = 0; kt < 8; ++kt) st[kt] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sp + kappa(kt, 0)));
     }
   }
   uint16_t* obase = mrun ? oi : out;
@@ -1771,8 +1773,13 @@ __device__ __forceinline__ void split_items(
       float* dst = slot < 0 ? new_state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState
                             : slotb + (static_cast<size_t>(slot) * kVHeads + h) * kHeadState;
       dst += static_cast<size_t>(vcol + l16) * kDim;
+      if (slot < 0) {
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(dst + kappa(kt, 0)) = st[kt];
+        for (int kt = 0; kt < 8; ++kt) __builtin_nontemporal_store(st[kt], reinterpret_cast<f32x4*>(dst + kappa(kt, 0)));
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) *reinterpret_cast<f32x4*>(dst + kappa(kt, 0)) = st[kt];
+      }
     } else {
       // M^T fragments: element (k, k') of M^T goes to fragment (k >> 4, d), lane
       // 16 lg' + (k & 15), slot s with k' = perm_depth(d, lg', s).  This wave
