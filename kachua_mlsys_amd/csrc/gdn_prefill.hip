@@ -644,9 +644,11 @@ __device__ __forceinline__ int kq_swz(int t) {
 }
 
 // 16 bytes per lane from global memory straight into LDS: lane i of the wave
-// writes bytes [16 i, 16 i + 16) after the wave-uniform LDS address.
+// writes bytes [16 i, 16 i + 16) after the wave-uniform LDS address.  AUX is
+// the cache policy: 2 (nt) streams data that is read exactly once.
+template <int AUX = 0>
 __device__ __forceinline__ void dma16(const void* src, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, 0);
+  __builtin_amdgcn_global_load_lds(src, lds_wave_base, 16, 0, AUX);
 }
 
 typedef __attribute__((ext_vector_type(4))) short i16x4;
@@ -1083,13 +1085,13 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
     const uint32_t off = row * (kQKHeads * kDim * 2) + dl.kq_col;
     dma16(kb + off, &sm.ks[P][32 * j + 4 * w][0]);
     dma16(qb + off, &sm.qs[P][32 * j + 4 * w][0]);
-    dma16(vb + row * (kVHeads * kDim * 2) + dl.v_col, &sm.vs[P][32 * j + 4 * w][0]);
+    dma16<2>(vb + row * (kVHeads * kDim * 2) + dl.v_col, &sm.vs[P][32 * j + 4 * w][0]);   // read once
   }
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
   const char* fb = reinterpret_cast<const char*>(ws_frag + rh * kFrags * kFragElems);
 #pragma unroll
   for (int j = 0; j < kFrags; ++j)
-    dma16(fb + (512 * j + 64 * w + lane) * 16, &sm.frag[P][0][0] + (512 * j + 64 * w) * 8);
+    dma16<2>(fb + (512 * j + 64 * w + lane) * 16, &sm.frag[P][0][0] + (512 * j + 64 * w) * 8);   // read once
   if (w == 0)   // gam, tail and the map bound: one 1 KB block
     dma16(reinterpret_cast<const char*>(ws_gam + rh * kGamStride) + 16 * lane, &sm.gt[P][0]);
 }
