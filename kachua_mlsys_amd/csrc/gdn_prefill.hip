@@ -1869,29 +1869,46 @@ union FinishLds {
   u32x4 frag[8][4][64];            // S as correction A fragments: [v-tile][d][lane], slot s = S[16 vt + l16][32 d + 8 lg + s]
 };
 
+// One slot state (64 KB, row-major) into registers, thread tid taking the
+// 16-byte pieces tid + e * kFinThreads.
+constexpr int kFinPer = kDim * kDim / 4 / kFinThreads;
+__device__ __forceinline__ void load_slot(const float* __restrict__ src, f32x4 (&t)[kFinPer]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int e = 0; e < kFinPer; ++e) {
+    const int q4 = tid + e * kFinThreads;
+    t[e] = *reinterpret_cast<const f32x4*>(src + (q4 >> 5) * kDim + (q4 & 31) * 4);
+  }
+}
+
 // State before segment j of the sequence whose slots start at g0, v-head h,
-// into sm.s (fp32).
+// into sm.s (fp32).  S_{i+1} is exactly slotb[g0 + i] for i = 0 (S_1) and after
+// a negligible map (B_i), so the rebuild starts from the latest such slot.  The
+// caller has loaded the usual one: `first` = slotb[g0 + j - 1], `prev` = the
+// M-run entry of segment j - 1 (any value with kMNegligible set when j = 1).
 __device__ void state_before(FinishLds& sm, int g0, int j, int h, const float* __restrict__ slotb,
-                             const uint16_t* __restrict__ slotm, const int* __restrict__ mval, int w, int lane) {
+                             const uint16_t* __restrict__ slotm, const int* __restrict__ mval, int w, int lane,
+                             const f32x4 (&first)[kFinPer], int prev) {
   const int tid = threadIdx.x;
   const int l16 = lane & 15, lg = lane >> 4;
-  int i0 = j - 1;   // S_{i0+1} is exactly slotb[g0 + i0]: S_1, or B_{i0} after a negligible map
-  while (i0 > 0 && (mval[static_cast<size_t>(g0 + i0) * kVHeads + h] & kMNegligible) == 0) --i0;
-  {
-    // 64 KB: every load of the thread is issued before the first LDS write
-    const float* src = slotb + (static_cast<size_t>(g0 + i0) * kVHeads + h) * kHeadState;
-    constexpr int kPer = kDim * kDim / 4 / kFinThreads;
-    f32x4 t[kPer];
-#pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      const int q4 = tid + e * kFinThreads;
-      t[e] = *reinterpret_cast<const f32x4*>(src + (q4 >> 5) * kDim + (q4 & 31) * 4);
-    }
+  int i0 = j - 1;
+  if ((prev & kMNegligible) == 0) {
+    // segment j-1's map is not negligible: step back to the latest slot that is a state
+    --i0;
+    while (i0 > 0 && (mval[static_cast<size_t>(g0 + i0) * kVHeads + h] & kMNegligible) == 0) --i0;
+    f32x4 t[kFinPer];
+    load_slot(slotb + (static_cast<size_t>(g0 + i0) * kVHeads + h) * kHeadState, t);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) {
+    for (int e = 0; e < kFinPer; ++e) {
       const int q4 = tid + e * kFinThreads;
       *reinterpret_cast<f32x4*>(&sm.s[q4 >> 5][(q4 & 31) * 4]) = t[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kFinPer; ++e) {
+      const int q4 = tid + e * kFinThreads;
+      *reinterpret_cast<f32x4*>(&sm.s[q4 >> 5][(q4 & 31) * 4]) = first[e];
     }
   }
   __syncthreads();
@@ -1966,8 +1983,13 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
     if (item >= ncorr) {
       // new_state = S_nseg
       const int4 me = lv.multi[(item - ncorr) >> 3];
+      // the usual starting slot and the entry that says whether it is the state
+      const int jl = me.z;
+      const int prev = jl >= 2 ? mval[static_cast<size_t>(me.y + jl - 1) * kVHeads + h] : kMNegligible;
+      f32x4 slot0[kFinPer];
+      load_slot(slotb + (static_cast<size_t>(me.y + jl - 1) * kVHeads + h) * kHeadState, slot0);
       __syncthreads();   // the previous item's readers of sm are done
-      state_before(sm, me.y, me.z, h, slotb, slotm, mval, w, lane);
+      state_before(sm, me.y, jl, h, slotb, slotm, mval, w, lane, slot0, prev);
       float* dst = new_state + (static_cast<size_t>(me.x) * kVHeads + h) * kHeadState;
       for (int e = tid; e < kDim * kDim / 4; e += kFinThreads) {
         const int row = e >> 5, col = (e & 31) * 4;
@@ -1992,6 +2014,10 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
     bf16x8 b[4][4];   // [token tile][d]: OI rows as B fragments
     u32x2 o0[4][8];   // [token tile][value tile]: O0, four value columns
     __amdgpu_buffer_rsrc_t orc = buf_rsrc(out, 0);
+    // the usual starting slot of the state rebuild, loaded with the outputs
+    const int prev = j >= 2 ? mval[static_cast<size_t>(g0 + j - 1) * kVHeads + h] : kMNegligible;
+    f32x4 slot0[kFinPer];
+    load_slot(slotb + (static_cast<size_t>(g0 + j - 1) * kVHeads + h) * kHeadState, slot0);
     if (active) {
       const long long c0 = c0s + static_cast<long long>(ci) * kChunk;
       const int c = min(kChunk, tok - ci * kChunk);
@@ -2013,7 +2039,7 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
     }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();   // the previous item's readers of sm are done
-    state_before(sm, g0, j, h, slotb, slotm, mval, w, lane);
+    state_before(sm, g0, j, h, slotb, slotm, mval, w, lane, slot0, prev);
     // S -> bf16 correction fragments (in place: read, barrier, write)
     u32x4 fr[2][4];
 #pragma unroll
