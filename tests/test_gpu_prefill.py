@@ -60,6 +60,16 @@ def test_prefill_segmented_weak_decay(gpu, lengths):
     _check(p, gpu, f"prefill segmented weak decay {lengths}")
 
 
+@pytest.mark.parametrize("lengths,weak", [([32768], False), ([16384], True), ([12000, 9000, 50, 7000], True)])
+def test_prefill_very_long(gpu, lengths, weak):
+    # hundreds of chunks in one sequence: the planner's long segment lengths,
+    # many segments and, with near-1 decay, a scan across every segment map
+    p = prefill_inputs_from_lengths(lengths, seed=sum(lengths) % 997)
+    if weak:
+        p.A_log = torch.linspace(-8.0, -5.0, 8)
+    _check(p, gpu, f"prefill very long {lengths} weak={weak}")
+
+
 def test_prefill_large_batch_plan_launch(gpu):
     # more sequences than one planning work-group owns: the separate plan
     # launch numbers the records; one long sequence is still segmented
