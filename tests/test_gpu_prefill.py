@@ -78,6 +78,19 @@ def test_prefill_large_batch_plan_launch(gpu):
     _check(prefill_inputs_from_lengths(lengths, seed=77), gpu, "prefill 600 sequences (plan launch)")
 
 
+@pytest.mark.parametrize("case", ["2500 short", "1100 with long"])
+def test_prefill_many_sequences(gpu, case):
+    # more sequences than planning threads (each owns several), empty ones
+    # included; long sequences among many short ones share the plan launch
+    g = torch.Generator().manual_seed(9)
+    if case == "2500 short":
+        lengths = [int(x) for x in torch.randint(0, 40, (2500,), generator=g)]
+    else:
+        lengths = [int(x) for x in torch.randint(1, 65, (1100,), generator=g)]
+        lengths[5], lengths[700], lengths[1099] = 3000, 1200, 129
+    _check(prefill_inputs_from_lengths(lengths, seed=len(lengths)), gpu, f"prefill {case}")
+
+
 def test_prefill_segmented_state_none(gpu):
     p = prefill_inputs_from_lengths([1800, 900], seed=21)
     p.state = None
