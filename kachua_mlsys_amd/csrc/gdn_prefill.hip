@@ -1660,7 +1660,18 @@ __device__ __forceinline__ void split_items(
     float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval) {
   const int nitems = lv.hdr[0] * 2 * kVHeads;
   int* queue = lv.hdr + 8;
-  for (int item = wg; item < nitems;) {
+  // First items: when the groups take a whole first wave of 16 runs, the four
+  // items of one (run, q/k head) (two v-heads, two halves) go to groups on the
+  // same XCD (group id % 8), so the chunk's K / Q rows and both v-heads'
+  // fragments are fetched into one L2.  Item (run r, q/k head hq, v-head e of
+  // the pair, half) -> group 8 (4 (G / 8) + 2 e + half) + G % 8, G = 4 r + hq.
+  int first = wg;
+  if (nwg == kConsumerGroups && nitems >= kConsumerGroups) {
+    const int x = wg & 7, slot = wg >> 3;
+    const int G = 8 * (slot >> 2) + x, k = slot & 3;
+    first = 16 * (G >> 2) + 8 * (k & 1) + kGva * (G & 3) + (k >> 1);
+  }
+  for (int item = first; item < nitems;) {
   int claimed = 0;   // thread 0: the next item from the queue (once claimed)
   bool has_claim = false;
   auto claim = [&] {
