@@ -1225,9 +1225,8 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
 
 // Full-head consumer over the short-sequence list (sequences of at most one
 // chunk): work item = (list entry, v-head), item i on work-group wg = i mod
-// nwg.  nwg and the work-group's linear id are multiples of 8 apart, so v-head
-// h runs on XCD h (XCD = linear id % 8), where its prepass records were
-// written.  Items are software-pipelined so that the state and operand traffic
+// nwg (short_entry / short_head).  nwg and the work-group's linear id are
+// multiples of 8 apart, so item i runs on XCD i % 8.  Items are software-pipelined so that the state and operand traffic
 // of one item overlaps the compute of the previous one: item k computes from
 // LDS buffer k & 1 and its state registers while item k+1's state loads and
 // operand copies (into the other buffer) are in flight and item k+2's list
@@ -1240,11 +1239,24 @@ struct ShortItem {
   long long c0;
 };
 
+// Item i of the short list -> (list entry, v-head).  Items run on work-group
+// i mod nwg, whose XCD is i % 8.  Within each block of 16 items (two entries)
+// XCD x takes both v-heads of q/k head x % 4 of one entry, so the two v-heads
+// that read the same K / Q rows share an L2; a last odd entry keeps the plain
+// order (entry i / 8, v-head i % 8).
+__device__ __forceinline__ int short_entry(int i, int nseq) {
+  const int blk = i >> 4;
+  return 2 * blk + 1 < nseq ? 2 * blk + ((i & 7) >> 2) : i >> 3;
+}
+__device__ __forceinline__ int short_head(int i, int nseq) {
+  return 2 * (i >> 4) + 1 < nseq ? 2 * (i & 3) + ((i >> 3) & 1) : i & 7;
+}
+
 // The list entry arrives in VGPRs (see entry() below) and becomes scalar here.
-__device__ __forceinline__ ShortItem short_item(const int4& e, int item) {
+__device__ __forceinline__ ShortItem short_item(const int4& e, int item, int nseq) {
   ShortItem it;
   it.s = __builtin_amdgcn_readfirstlane(e.x);
-  it.h = item & 7;
+  it.h = short_head(item, nseq);
   it.rec = __builtin_amdgcn_readfirstlane(e.y);
   const int zw = __builtin_amdgcn_readfirstlane(e.w);
   it.c = zw >> 16;
@@ -1300,10 +1312,10 @@ __device__ __forceinline__ void full_head_items(
   // does not wait for the loads and copies issued after it.
   int zero_v;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero_v));
-  auto entry = [&](int i) { return list[((i < nitems ? i : 0) >> 3) + zero_v]; };
+  auto entry = [&](int i) { return list[short_entry(i < nitems ? i : 0, nseq) + zero_v]; };
 
   int item = wg;
-  ShortItem cur = short_item(entry(item), item);
+  ShortItem cur = short_item(entry(item), item, nseq);
   f32x4 st[8];
   issue(cur, st, std::integral_constant<int, 0>{});
   int4 enext = entry(item + nwg);
@@ -1316,7 +1328,7 @@ __device__ __forceinline__ void full_head_items(
     lds_barrier();                         // ... in every wave
     const int inext = item + nwg;
     const bool has_next = inext < nitems;
-    const ShortItem nx = short_item(enext, inext);
+    const ShortItem nx = short_item(enext, inext, nseq);
     f32x4 stn[8];
     if (has_next) issue(nx, stn, std::integral_constant<int, P ^ 1>{});
     enext = entry(inext + nwg);
