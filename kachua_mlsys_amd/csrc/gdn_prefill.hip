@@ -103,13 +103,14 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 // in one entry, so an item costs one dependent load before its data.
 //   hdr[0] runs, [1] short sequences, [2] segment length L (chunks),
 //   [3] multi-segment sequences, [4] segments >= 1 over all sequences,
-//   [8] split-consumer work queue (items claimed past each group's first)
+//   [8] split-consumer work queue (items claimed past each group's first),
+//   [9] correction blocks appended by the consumer's M-runs
 //   multi[e]   = (seq, first slot, segments, 0)
 //   segs[i]    = (first token lo, hi, tokens in the segment | j << 17, slot of
 //                 segment j - 1) for every segment j >= 1 (L <= 1024 chunks:
 //                 at most 65536 tokens)
-//   runs[2i]   = (seq, flags | tokens of the run's last chunk << 8,
-//                 final-state slot or -1 for new_state, first record)
+//   runs[2i]   = (seq, flags | tokens of the run's last chunk << 8 | segment
+//                 j << 16, final-state slot or -1 for new_state, first record)
 //   runs[2i+1] = (first token lo, hi, chunks with records, chunks)
 //   flags: kRunM (M-run), kRunFromState (initial state from `state`)
 //   shorts[i]  = (seq, record of its chunk or -1 when it has none, first token
@@ -118,6 +119,14 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 constexpr int kListHdr = 16;
 constexpr int kRunM = 1;
 constexpr int kRunFromState = 2;
+
+// Finish work: a correction block is kFinChunks chunks of one (segment, v-head);
+// the four waves of a finish group split its chunks, then a chunk's 16-token tiles.
+constexpr int kFinThreads = 256;
+constexpr int kFinChunks = 1;                             // chunks per correction block
+constexpr int kFinWpc = kFinThreads / 64 / kFinChunks;    // waves per chunk
+constexpr int kFinTpw = kChunk / 16 / kFinWpc;            // 16-token tiles per wave
+static_assert(kFinWpc * kFinChunks == kFinThreads / 64 && kFinTpw * kFinWpc == kChunk / 16, "finish tiling");
 __host__ __device__ inline long long max_runs(int num_seqs, long long gcap) { return 2 * gcap + num_seqs; }
 
 struct ListView {
@@ -154,6 +163,7 @@ struct WsLayout {
   size_t slotm_off;    // u16  [G][8][kMSlotElems] M_j^T fragments
   size_t oi_off;       // u16  [T][8][128]       M-run outputs OI (rows of segments >= 1)
   size_t mval_off;     // i32  [G][8]            M-run chunks whose outputs OI were formed | kMNegligible
+  size_t fix_off;      // i32x4[8 R][2]          correction blocks (segs entry; v-head, first, last chunk)
   size_t total;
 };
 
@@ -178,6 +188,8 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   L.slotm_off = off; off = align256(off + G * kVHeads * kMSlotElems * sizeof(uint16_t));
   L.oi_off = off;    off = align256(off + static_cast<size_t>(tokens) * kVHeads * kDim * sizeof(uint16_t));
   L.mval_off = off;  off = align256(off + G * kVHeads * sizeof(int));
+  // a block covers formed chunks of one M-run, whose records are its own: at most 8 R blocks
+  L.fix_off = off;   off = align256(off + R * kVHeads * 2 * sizeof(int4));
   L.total = off;
   return L;
 }
@@ -516,7 +528,10 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       ps[kPsCur + b0_] = ex;
       ps[kPsCur + b1_] = ex + h0;
     }
-    if (lane == 0) lv.hdr[8] = 0;   // work queue
+    if (lane == 0) {
+      lv.hdr[8] = 0;   // work queue
+      lv.hdr[9] = 0;   // correction blocks
+    }
     if (lane == 63) {
       lv.hdr[0] = tot[4] + inc;
       lv.hdr[1] = tot[1];
@@ -573,7 +588,8 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       const int nvalid = static_cast<int>(max(0LL, min(static_cast<long long>(nrun), R - rfirst)));
       const int flags = (mrun ? kRunM : 0) | (!mrun && j == 0 ? kRunFromState : 0);
       const int slot = p.multi ? g0 + j : -1;
-      lv.runs[2 * pos] = make_int4(s, flags | (last_tok << 8), slot, static_cast<int>(min(rfirst, 0x7fffffffLL)));
+      lv.runs[2 * pos] = make_int4(s, flags | (last_tok << 8) | (j << 16), slot,
+                                   static_cast<int>(min(rfirst, 0x7fffffffLL)));
       lv.runs[2 * pos + 1] = make_int4(static_cast<int>(c0 & 0xffffffffLL), static_cast<int>(c0 >> 32), nvalid, nrun);
     };
     for (int j = 0; j < p.full_seg; ++j) {
@@ -1669,7 +1685,8 @@ __device__ __forceinline__ void split_items(
     const float* __restrict__ state, float scale, const uint16_t* __restrict__ ws_frag,
     const float* __restrict__ ws_gam,
     uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
-    float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval) {
+    float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval, int4* __restrict__ fix,
+    int fix_cap) {
   const int nitems = lv.hdr[0] * 2 * kVHeads;
   int* queue = lv.hdr + 8;
   // First items: when the groups take a whole first wave of 16 runs, the four
@@ -1683,6 +1700,7 @@ __device__ __forceinline__ void split_items(
     const int G = 8 * (slot >> 2) + x, k = slot & 3;
     first = 16 * (G >> 2) + 8 * (k & 1) + kGva * (G & 3) + (k >> 1);
   }
+  constexpr int kFixLane = 4 * 64;   // a side-wave lane appends the M-runs' correction blocks
   for (int item = first; item < nitems;) {
   int claimed = 0;   // thread 0: the next item from the queue (once claimed)
   bool has_claim = false;
@@ -1694,12 +1712,22 @@ __device__ __forceinline__ void split_items(
   };
   const int h = item & 7;
   const int hv = (item >> 3) & 1;
-  const int4 ra = lv.runs[2 * (item >> 4)];
-  const int4 rb = lv.runs[2 * (item >> 4) + 1];
+  // The run table was written by an earlier launch and is constant here, so
+  // it is read through the constant address space: scalar loads, counted in
+  // lgkmcnt.  Vector loads would count in vmcnt behind the previous item's
+  // final-state stores, and waiting for the descriptor would wait for those.
+  const auto* runs_c = (const __attribute__((address_space(4))) u32x4*)lv.runs;
+  const u32x4 ua = runs_c[2 * (item >> 4)];
+  const u32x4 ub = runs_c[2 * (item >> 4) + 1];
+  const int4 ra = make_int4(static_cast<int>(ua.x), static_cast<int>(ua.y), static_cast<int>(ua.z),
+                            static_cast<int>(ua.w));
+  const int4 rb = make_int4(static_cast<int>(ub.x), static_cast<int>(ub.y), static_cast<int>(ub.z),
+                            static_cast<int>(ub.w));
   const int s = ra.x, slot = ra.z, rfirst = ra.w;
   const bool mrun = (ra.y & kRunM) != 0;
   const bool from_state = (ra.y & kRunFromState) != 0;
-  const int last_tok = min(ra.y >> 8, kChunk);   // the chunk length indexes 64-entry LDS rows
+  const int last_tok = min((ra.y >> 8) & 0xff, kChunk);   // the chunk length indexes 64-entry LDS rows
+  const int jseg = ra.y >> 16;
   const long long c0r = static_cast<long long>(static_cast<unsigned>(rb.x)) | (static_cast<long long>(rb.y) << 32);
   const int n = rb.z, nrun = rb.w;
   const int hq = h / kGva;
@@ -1737,6 +1765,15 @@ __device__ __forceinline__ void split_items(
                     static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
   };
   const SplitDmaLane dl = split_dma_lane(wt, lane, hv);
+  // Correction blocks of the segment: chunks [0, formed) get O0 + OI S_j^T in
+  // the finish.  Each M-run (once per v-head) reserves a block per kFinChunks
+  // chunks with records during its first chunk (the atomic returns before
+  // that chunk's closing barrier, with the next chunk's copies), and fills
+  // them at its end, blocks past `formed` left empty.  The finish then takes
+  // one block per group with a single descriptor load.  The entry repeats the
+  // later-segment table's.
+  const int fix_max = (n + kFinChunks - 1) / kFinChunks;
+  int fix_pos = 0;
 
   // An M-run stops once the bound of its map falls below kNegligibleLog2: its
   // outputs of later chunks are negligible (the correction skips them) and so
@@ -1754,6 +1791,7 @@ __device__ __forceinline__ void split_items(
       split_dma<0>(sm, chunk_ref(0), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
     }
     __syncthreads();
+    if (mrun && hv == 0 && tid == kFixLane) fix_pos = atomicAdd(lv.hdr + 9, fix_max);
     for (int i = 0; i < n; i += 2) {
       {
         if (i + 1 >= n) claim();
@@ -1792,6 +1830,13 @@ __device__ __forceinline__ void split_items(
     }
   }
   if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed | (formed < n ? kMNegligible : 0);
+  if (mrun && hv == 0 && tid == kFixLane && fix_max > 0) {
+    const int4 seg = make_int4(rb.x, rb.y, ((nrun - 1) * kChunk + last_tok) | (jseg << 17), slot - 1);
+    for (int b = 0; b < fix_max && fix_pos + b < fix_cap; ++b) {
+      fix[2 * (fix_pos + b)] = seg;
+      fix[2 * (fix_pos + b) + 1] = make_int4(h, b * kFinChunks, min((b + 1) * kFinChunks, formed), 0);
+    }
+  }
 
   if (chain && !(mrun && formed < n)) {   // a stopped M-run's map is negligible: never read
     if (slot < 0 || !mrun) {
@@ -1851,13 +1896,14 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
                      const int* __restrict__ rec_start, int* __restrict__ lists, int num_seqs,
                      int g_long, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
                      uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
-                     float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval) {
+                     float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval,
+                     int4* __restrict__ fix) {
   __shared__ ConsumerLds sm;
   const int bid = blockIdx.x;
   const ListView lv = list_view(lists, num_seqs, gcap);
   if (bid < g_long) {
     split_items(sm.split, bid, g_long, lv, q, k, v, state, scale, ws_frag, ws_gam, out, new_state, oi, slotb,
-                slotm, mval);
+                slotm, mval, fix, R * kVHeads);
     // an M-run that stopped early may leave its next chunk's copies into LDS in
     // flight: they land before the work-group releases its LDS
     __builtin_amdgcn_s_waitcnt(0);
@@ -1875,16 +1921,16 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 // B_j itself: the state before segment j is rebuilt from the latest such
 // segment before it (or from S_1), with scan steps only across segments whose
 // maps are not negligible.  Work items, one work-group each:
-//   (segment j >= 1, block of kFinChunks chunks, v-head): S_j, then out =
-//        bf16(O0 + OI S_j^T) for the block's chunks whose OI was formed (the
-//        rest keep O0), wave w taking chunk w of the block;
+//   a correction block (segment j >= 1, v-head, kFinChunks chunks whose OI was
+//        formed), as the consumer's M-run appended it: S_j, then out =
+//        bf16(O0 + OI S_j^T) for the block's chunks (the other chunks keep
+//        O0); the four waves split the block's chunks, and within a chunk its
+//        four 16-token tiles;
 //   (multi-segment sequence, v-head): new_state = S_nseg.
 // A scan step forms D = M^T S^T on MFMA with M^T as the M-run stored it (bf16
 // hi / lo) and S split into hi / lo from LDS (three products, fp32
 // accumulation from B_i).  The correction multiplies OI (bf16) by S as a single
 // bf16, as the chunk recurrence does in Q S^T.
-constexpr int kFinThreads = 256;
-constexpr int kFinChunks = 4;
 constexpr int kFinRow = kDim + 4;   // floats per LDS row of S
 
 union FinishLds {
@@ -1986,6 +2032,7 @@ __device__ void state_before(FinishLds& sm, int g0, int j, int h, const float* _
 }
 
 __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ lists, int num_seqs, int gcap,
+                                                             const int4* __restrict__ fix, int fix_cap,
                                                              const float* __restrict__ slotb,
                                                              const uint16_t* __restrict__ slotm,
                                                              const int* __restrict__ mval,
@@ -1994,18 +2041,20 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
                                                              float* __restrict__ new_state) {
   __shared__ FinishLds sm;
   const ListView lv = list_view(lists, num_seqs, gcap);
-  const int nmulti = lv.hdr[3], nsegs = lv.hdr[4], L = lv.hdr[2];
-  const int per_seg = (L + kFinChunks - 1) / kFinChunks;   // blocks per segment
-  const int ncorr = nsegs * per_seg * kVHeads;
+  const int nmulti = lv.hdr[3];
+  const int ncorr = min(lv.hdr[9], fix_cap);   // correction blocks
+  // the blocks were written by the consumer launch: constant here (scalar loads)
+  const auto* fix_c = (const __attribute__((address_space(4))) u32x4*)fix;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int l16 = lane & 15, lg = lane >> 4;
-  for (int item = blockIdx.x; item < ncorr + nmulti * kVHeads; item += gridDim.x) {
-    const int h = item & 7;
-    if (item >= ncorr) {
+  // the state items first: they may step through several segment maps
+  for (int it = blockIdx.x; it < ncorr + nmulti * kVHeads; it += gridDim.x) {
+    if (it < nmulti * kVHeads) {
+      const int h = it & 7;
       // new_state = S_nseg
-      const int4 me = lv.multi[(item - ncorr) >> 3];
+      const int4 me = lv.multi[it >> 3];
       // the usual starting slot and the entry that says whether it is the state
       const int jl = me.z;
       const int prev = jl >= 2 ? mval[static_cast<size_t>(me.y + jl - 1) * kVHeads + h] : kMNegligible;
@@ -2020,22 +2069,26 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
       }
       continue;
     }
-    const int u = item >> 3;
-    const int4 sg = lv.segs[u / per_seg];
+    // block: (first token lo, hi, tokens | j << 17, slot of segment j - 1) and
+    // (v-head, first chunk, end chunk): chunks [first, last) need OI S_j^T
+    const int item = it - nmulti * kVHeads;
+    const u32x4 fa = fix_c[2 * item], fb = fix_c[2 * item + 1];
+    const int4 sg = make_int4(static_cast<int>(fa.x), static_cast<int>(fa.y), static_cast<int>(fa.z),
+                              static_cast<int>(fa.w));
+    const int h = static_cast<int>(fb.x) & 7;
     const int tok = sg.z & ((1 << 17) - 1), j = sg.z >> 17;
     const int g0 = sg.w - (j - 1);
-    const int first = (u % per_seg) * kFinChunks;   // first chunk of the block within the segment
-    const int nchunks = (tok + kChunk - 1) / kChunk;
-    const int formed = mval[static_cast<size_t>(g0 + j) * kVHeads + h] & (kMNegligible - 1);
-    const int last = min(min(first + kFinChunks, nchunks), formed);   // chunks [first, last) need OI S^T
+    const int first = static_cast<int>(fb.y);
+    const int last = min(static_cast<int>(fb.z), (tok + kChunk - 1) / kChunk);
     if (first >= last) continue;
-    // wave w corrects chunk first + w (all 64 tokens, all 128 value rows); its
-    // OI and O0 loads are issued before the state is formed
+    // wave w corrects token tiles [tt0, tt0 + kFinTpw) of chunk first + w / kFinWpc
+    // (all 128 value rows); its OI and O0 loads are issued before the state is formed
     const long long c0s = static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32);
-    const int ci = first + w;
+    const int ci = first + w / kFinWpc;
+    const int tt0 = (w % kFinWpc) * kFinTpw;
     const bool active = ci < last;
-    bf16x8 b[4][4];   // [token tile][d]: OI rows as B fragments
-    u32x2 o0[4][8];   // [token tile][value tile]: O0, four value columns
+    bf16x8 b[kFinTpw][4];   // [token tile][d]: OI rows as B fragments
+    u32x2 o0[kFinTpw][8];   // [token tile][value tile]: O0, four value columns
     __amdgpu_buffer_rsrc_t orc = buf_rsrc(out, 0);
     // the usual starting slot of the state rebuild, loaded with the outputs
     const int prev = j >= 2 ? mval[static_cast<size_t>(g0 + j - 1) * kVHeads + h] : kMNegligible;
@@ -2049,8 +2102,8 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
       orc = buf_rsrc(out + rowbase, bytes);
       const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const uint32_t trow = static_cast<uint32_t>(16 * tt + l16) * (kVHeads * kDim * 2);
+      for (int tt = 0; tt < kFinTpw; ++tt) {
+        const uint32_t trow = static_cast<uint32_t>(16 * (tt0 + tt) + l16) * (kVHeads * kDim * 2);
 #pragma unroll
         for (int d = 0; d < 4; ++d)
           b[tt][d] = __builtin_bit_cast(
@@ -2084,22 +2137,22 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
     if (active) {
 #pragma unroll
       for (int vt = 0; vt < 8; ++vt) {
-        // four independent accumulators (token tiles)
-        f32x4 acc[4];
+        // independent accumulators (token tiles)
+        f32x4 acc[kFinTpw];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int tt = 0; tt < kFinTpw; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
           const bf16x8 a_ = __builtin_bit_cast(bf16x8, sm.frag[vt][d][lane]);
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt) acc[tt] = mfma16(a_, b[tt][d], acc[tt]);
+          for (int tt = 0; tt < kFinTpw; ++tt) acc[tt] = mfma16(a_, b[tt][d], acc[tt]);
         }
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt) {
+        for (int tt = 0; tt < kFinTpw; ++tt) {
           const u32x2 o = o0[tt][vt];
           const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[tt][0], bf_hi(o.x) + acc[tt][1]),
                             pack_bf2(bf_lo(o.y) + acc[tt][2], bf_hi(o.y) + acc[tt][3])};
-          const uint32_t trow = static_cast<uint32_t>(16 * tt + l16) * (kVHeads * kDim * 2);
+          const uint32_t trow = static_cast<uint32_t>(16 * (tt0 + tt) + l16) * (kVHeads * kDim * 2);
           __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
         }
       }
@@ -2134,7 +2187,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   const long long R = max_records(num_seqs, total_tokens);
   const long long gcap = max_segments(total_tokens);
   // every work-item index (records x heads, runs x 16, multi-segment entries x 64) fits an int
-  if (R * kVHeads > 0x7fffffffLL || static_cast<long long>(num_seqs) * kVHeads * 8 > 0x7fffffffLL ||
+  if (R * kVHeads + static_cast<long long>(num_seqs) * kVHeads * 8 > 0x7fffffffLL ||
       max_runs(num_seqs, gcap) * 2 * kVHeads > 0x7fffffffLL)
     return GDN_ERR_INVALID_ARGUMENT;
   const WsLayout L = ws_layout(num_seqs, total_tokens);
@@ -2151,6 +2204,7 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   auto* slotm = reinterpret_cast<uint16_t*>(ws + L.slotm_off);
   auto* oi = reinterpret_cast<uint16_t*>(ws + L.oi_off);
   auto* mval = reinterpret_cast<int*>(ws + L.mval_off);
+  auto* fix = reinterpret_cast<int4*>(ws + L.fix_off);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const auto* qb = static_cast<const uint16_t*>(q);
   const auto* kb = static_cast<const uint16_t*>(k);
@@ -2177,12 +2231,12 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   const long long g_short = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads, kConsumerGroups);
   consumer_kernel<<<dim3(static_cast<unsigned>(g_long + g_short)), dim3(kSplitThreads), 0, st>>>(
       qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, Ri, gc, scale, rec_start, lists,
-      num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm, mval);
+      num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm, mval, fix);
   // a second segment needs more than kMinSegChunks chunks in one sequence
   if (total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
     const long long g_fin = std::min<long long>(R * kVHeads, 1024);
-    finish_kernel<<<dim3(static_cast<unsigned>(g_fin)), dim3(kFinThreads), 0, st>>>(lists, num_seqs, gc, slotb, slotm,
-                                                                                     mval, oi, ob, new_state);
+    finish_kernel<<<dim3(static_cast<unsigned>(g_fin)), dim3(kFinThreads), 0, st>>>(
+        lists, num_seqs, gc, fix, static_cast<int>(R * kVHeads), slotb, slotm, mval, oi, ob, new_state);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
