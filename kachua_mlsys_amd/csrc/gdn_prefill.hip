@@ -1701,12 +1701,18 @@ __device__ __forceinline__ void split_items(
     first = 16 * (G >> 2) + 8 * (k & 1) + kGva * (G & 3) + (k >> 1);
   }
   constexpr int kFixLane = 4 * 64;   // a side-wave lane appends the M-runs' correction blocks
+  // The queue and block counters are bumped by one lane.  An opaque zero
+  // offset keeps the compiler from rewriting these atomics into the
+  // wave-aggregated form, whose result broadcast waits for the atomic on the
+  // spot; the plain atomic is waited for where its result is first used.
+  int zero_v;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero_v));
   for (int item = first; item < nitems;) {
   int claimed = 0;   // thread 0: the next item from the queue (once claimed)
   bool has_claim = false;
   auto claim = [&] {
     if (threadIdx.x == 0 && !has_claim) {
-      claimed = nwg + atomicAdd(queue, 1);
+      claimed = atomicAdd(queue + zero_v, 1);   // queue position: item nwg + claimed
       has_claim = true;
     }
   };
@@ -1791,7 +1797,7 @@ __device__ __forceinline__ void split_items(
       split_dma<0>(sm, chunk_ref(0), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
     }
     __syncthreads();
-    if (mrun && hv == 0 && tid == kFixLane) fix_pos = atomicAdd(lv.hdr + 9, fix_max);
+    if (mrun && hv == 0 && tid == kFixLane) fix_pos = atomicAdd(lv.hdr + 9 + zero_v, fix_max);
     for (int i = 0; i < n; i += 2) {
       {
         if (i + 1 >= n) claim();
@@ -1828,7 +1834,14 @@ __device__ __forceinline__ void split_items(
         }
       }
     }
+  } else {
+    lds_barrier();   // every wave has read this item's index before it is replaced
   }
+  // The next item is published before the final-state stores: reading the
+  // claim's result waits for every earlier vector-memory operation of the
+  // wave, and the stores would be among them.
+  claim();
+  if (threadIdx.x == 0) sm.next_item = nwg + claimed;
   if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed | (formed < n ? kMNegligible : 0);
   if (mrun && hv == 0 && tid == kFixLane && fix_max > 0) {
     const int4 seg = make_int4(rb.x, rb.y, ((nrun - 1) * kChunk + last_tok) | (jseg << 17), slot - 1);
@@ -1873,8 +1886,6 @@ __device__ __forceinline__ void split_items(
       }
     }
   }
-  claim();
-  if (threadIdx.x == 0) sm.next_item = claimed;
   lds_barrier();   // publishes the next item; the item's stores stay in flight
   item = sm.next_item;
   }
