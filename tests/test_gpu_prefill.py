@@ -197,3 +197,24 @@ def test_prefill_overlapping_cu_seqlens_is_safe(gpu):
     o_ref, s_ref = prefill_ref(*p.args())
     assert state_rel(ns[0], s_ref[0]) <= 2e-3
     assert torch.isfinite(ns).all()
+
+
+def test_prefill_exhausted_records_is_safe(gpu):
+    # overlapping cu_seqlens that ask for more chunks (2 x 64) than the
+    # workspace has records (T / 64 + N = 67): the third sequence keeps 3 of
+    # its 64 chunks, its later segments run with no chunk at all, and the call
+    # still completes with the first sequence exact
+    T = 4096
+    p = prefill_inputs_from_lengths([T], seed=14)
+    cu = torch.tensor([0, T, 0, T], dtype=torch.int32)
+    state = torch.randn(3, 8, 128, 128, generator=torch.Generator().manual_seed(15)) * 0.02
+    state[0] = p.state[0]
+    g = p.to(gpu)
+    print("[case] exhausted records: cu_seqlens [0, 4096, 0, 4096], T = 4096", flush=True)
+    out, ns = prefill.launch_gdn(g.q, g.k, g.v, state.to(gpu), g.A_log, g.a, g.dt_bias, g.b,
+                                 cu.to(gpu), None)
+    torch.cuda.synchronize()
+    o_ref, s_ref = prefill_ref(*p.args())
+    assert state_rel(ns[0], s_ref[0]) <= 2e-3
+    assert torch.isfinite(ns).all()
+    assert not ns[1].any()   # the decreasing pair is an empty sequence
