@@ -270,7 +270,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "the decode and prefill paths shard with no exchange, see DESIGN.md", file=sys.stderr)
+              "sequences (and their states) are independent, so the decode and prefill paths "
+              "would shard by sequence with no exchange between GPUs", file=sys.stderr)
         sys.exit(2)
 
     import torch
