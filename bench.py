@@ -114,7 +114,7 @@ def time_launches(fn, sets, steps, warmup, torch):
 
 
 def hbm_copy_gbps(torch, dev, nbytes=1 << 30, reps=10):
-    """Achievable HBM bandwidth: device-to-device copy of `nbytes` (read + write)."""
+    """torch's device-to-device copy of `nbytes` (read + write GB/s), for comparison."""
     src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -129,6 +129,45 @@ def hbm_copy_gbps(torch, dev, nbytes=1 << 30, reps=10):
     ms = s.elapsed_time(e) / reps
     del src, dst
     return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def hbm_stream_gbps(torch, dev, nbytes=1 << 30, reps=10):
+    """Achievable HBM bandwidth from the hand-written streaming kernel
+    (csrc/hbm_stream.hip: 16-byte non-temporal loads and stores, 8 loads in
+    flight per lane), best over a sweep of grid sizes and loads in flight.
+    1 GiB each way, far beyond the 256 MiB Infinity Cache.  Returns (GB/s
+    read + write, launch shape)."""
+    from kachua_mlsys_amd import _lib
+
+    probe = _lib.load_probe()
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream(dev)
+    n16 = nbytes // 16
+    best = (0.0, None)
+    for groups, unroll in ((512, 8), (1024, 4), (1024, 8), (2048, 4), (2048, 8), (4096, 4), (1024, 16)):
+        def run():
+            st = probe.hbm_stream_copy(src.data_ptr(), dst.data_ptr(), n16, groups, unroll,
+                                       stream.cuda_stream)
+            if st != 0:
+                raise RuntimeError(f"hbm_stream_copy failed with status {st}")
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            run()
+        e.record(stream)
+        torch.cuda.synchronize()
+        gbps = 2 * nbytes / (s.elapsed_time(e) / reps * 1e-3) / 1e9
+        if gbps > best[0]:
+            best = (gbps, {"groups": groups, "loads_in_flight_per_lane": unroll})
+    ok = bool(torch.equal(dst[:1 << 20], src[:1 << 20]))
+    del src, dst
+    if not ok:
+        raise RuntimeError("hbm_stream_copy produced a wrong copy")
+    return best
 
 
 def cpu_decode_baseline(torch, B=64, min_seconds=8.0):
@@ -175,16 +214,17 @@ def cpu_prefill_baseline(torch, p, max_tokens=1 << 30):
                       f"({tot} tokens) of the workload, {t:.2f} s"}
 
 
-def time_prefill(p_cpu, args, torch, dev, traffic=None) -> dict:
+def time_prefill(p_cpu, args, torch, dev, traffic=None, warm=None) -> dict:
     """One prefill workload: µs per call (HIP-graph replay, rotated buffer
-    sets), tokens/s and its roofline."""
+    sets unless warm), tokens/s and its roofline."""
     from kachua_mlsys_amd import prefill
 
+    warm = args.warm_cache if warm is None else warm
     p = p_cpu.to(dev)
     T, N = p.q.shape[0], len(p.lengths)
     ws = torch.empty(prefill.workspace_bytes(N, T), dtype=torch.uint8, device=dev)
     per_set = prefill_bytes(T, N) + ws.numel()
-    nsets = 1 if args.warm_cache else max(2, math.ceil(2 * MALL_BYTES / per_set) + 1)
+    nsets = 1 if warm else max(2, math.ceil(2 * MALL_BYTES / per_set) + 1)
     sets = []
     for i in range(nsets):
         q, k, v = (p.q, p.k, p.v) if i == 0 else (p.q.clone(), p.k.clone(), p.v.clone())
@@ -219,11 +259,25 @@ def time_prefill(p_cpu, args, torch, dev, traffic=None) -> dict:
                      "algorithmic_bytes": nbytes, "algorithmic_flops": flops,
                      "tflops": round(flops / t_s / 1e12, 2),
                      "traffic": read_traffic(traffic) if traffic else None},
-        "cache": "warm" if args.warm_cache else f"cold ({nsets} rotated sets)",
+        "cache": "warm" if warm else f"cold ({nsets} rotated sets)",
     }
     del sets, ws
     torch.cuda.empty_cache()
     return entry
+
+
+def chain_step_us(args, torch, dev) -> dict:
+    """Time of one chunk step of the sequential state chain: one sequence of
+    4 chunks against one of 2 (warm cache; too short to be cut into segments,
+    so the difference is two chunk steps of the consumer's chain)."""
+    from kachua_mlsys_amd.inputs import prefill_inputs_from_lengths
+
+    t = {}
+    for nch in (2, 4):
+        p = prefill_inputs_from_lengths([64 * nch], seed=11)
+        t[nch] = time_prefill(p, args, torch, dev, warm=True)["us_per_call"]
+    return {"us": round((t[4] - t[2]) / 2, 3), "us_per_call_2_chunks": t[2], "us_per_call_4_chunks": t[4],
+            "method": "(t(1 x 256 tokens) - t(1 x 128 tokens)) / 2, warm cache"}
 
 
 # Prefill shapes the reference published B200 timings for (contest workloads;
@@ -264,6 +318,11 @@ def main():
     ap.add_argument("--only", choices=["all", "decode", "prefill"], default="all",
                     help="restrict the run (for profiling)")
     ap.add_argument("--warm-cache", action="store_true", help="do not rotate buffers")
+    ap.add_argument("--prefill-configs", default="3,2,4",
+                    help="comma-separated prefill configurations to time (for profiling)")
+    ap.add_argument("--profile", action="store_true",
+                    help="time only the named workloads (no chain-step, warm-cache or bandwidth-probe "
+                         "launches), so counter runs see one workload per kernel")
     ap.add_argument("--reference-shapes", action="store_true",
                     help="instead of the headline line: prefill at the shapes the reference published "
                          "B200 timings for")
@@ -339,17 +398,43 @@ def main():
     # ----------------------------------------------------------- prefill ----
     if args.only in ("all", "prefill"):
         pre = {}
-        for cfg in (3, 2, 4):
+        cfgs = [int(c) for c in args.prefill_configs.split(",") if c.strip()]
+        step = (chain_step_us(args, torch, dev)
+                if any(c in (2, 3) for c in cfgs) and not args.profile else None)
+        for cfg in cfgs:
             p_cpu = prefill_config(cfg)
             entry = time_prefill(p_cpu, args, torch, dev, traffic=f"prefill_c{cfg}_traffic.txt")
+            if not args.warm_cache and not args.profile:
+                entry["us_per_call_warm"] = time_prefill(p_cpu, args, torch, dev, warm=True)["us_per_call"]
+            if cfg in (2, 3) and step is not None:
+                # sequential floor without segment parallelism: longest sequence's chunks x step
+                nch = math.ceil(entry["max_len"] / 64)
+                entry["critical_path_floor_us"] = round(nch * step["us"], 2)
+                entry["critical_path_chunks"] = nch
             if cfg == 3 and not args.no_cpu:
                 entry["cpu_baseline"] = cpu_prefill_baseline(torch, p_cpu)
             pre[f"c{cfg}"] = entry
+        if step is not None:
+            pre["chain_step"] = step
         result["prefill"] = pre
+        if "c3" in pre:
+            result["prefill_c3_us"] = pre["c3"]["us_per_call"]
+            result["prefill_c3_tokens_per_s"] = pre["c3"]["tokens_per_s"]
+            result["prefill_c3_roofline_frac"] = pre["c3"]["roofline"]["frac"]
 
     if args.only in ("all", "decode") and not args.no_cpu:
         result["cpu_baseline"] = cpu_decode_baseline(torch)
-    result["hbm_copy_GBps_measured"] = round(hbm_copy_gbps(torch, dev), 1)
+    if args.profile:
+        print(json.dumps(result), flush=True)
+        return
+    gbps, grid = hbm_stream_gbps(torch, dev)
+    result["hbm_stream_GBps_measured"] = {
+        "value": round(gbps, 1), "launch": grid,
+        "kernel": "stream_copy_kernel (csrc/hbm_stream.hip): 1 GiB read + 1 GiB written, "
+                  "16-byte non-temporal loads/stores"}
+    if "roofline" in result:
+        result["roofline"]["frac_of_measured_stream"] = round(result["roofline"]["achieved"] / gbps, 4)
+    result["hbm_copy_GBps_torch"] = round(hbm_copy_gbps(torch, dev), 1)
     result["host"] = {"cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
                       "device": torch.cuda.get_device_name(dev)}
     print(json.dumps(result), flush=True)

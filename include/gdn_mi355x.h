@@ -41,9 +41,9 @@ const char* gdn_status_string(int status);
  * of gdn_decode_qk4_v8_d128_k_last/solution/cuda/kernel.cu:982-1064 (argument
  * order kept); results follow solution/reference_torch_impl.py:11-72.
  *   q, k      [batch, 1, 4, 128] bf16   (8-byte aligned)
- *   v         [batch, 1, 8, 128] bf16
+ *   v         [batch, 1, 8, 128] bf16   (2-byte aligned, as are a, b, out)
  *   state     [batch, 8, 128, 128] fp32 (16-byte aligned; read only)
- *   A_log     [8] fp32,  dt_bias [8] fp32
+ *   A_log     [8] fp32,  dt_bias [8] fp32 (4-byte aligned)
  *   a, b      [batch, 1, 8] bf16
  *   scale     output scale; 0 selects 1/sqrt(128)
  *   out       [batch, 8, 128] bf16 (written)
@@ -68,14 +68,14 @@ size_t gdn_prefill_workspace_bytes(int num_seqs, long long total_tokens);
  * (argument order kept); results follow solution/reference_torch_impl.py:16-92,
  * including new_state = 0 for an empty sequence.
  *   q, k        [total_tokens, 4, 128] bf16 (16-byte aligned)
- *   v           [total_tokens, 8, 128] bf16
+ *   v           [total_tokens, 8, 128] bf16 (16-byte aligned)
  *   state       [num_seqs, 8, 128, 128] fp32 or NULL for zeros (16-byte aligned)
- *   A_log, dt_bias [8] fp32;  a, b [total_tokens, 8] bf16
- *   cu_seqlens  [num_seqs + 1] int32 (cu_seqlens_is_int64 == 0) or int64;
+ *   A_log, dt_bias [8] fp32 (4-byte aligned);  a, b [total_tokens, 8] bf16 (2-byte aligned)
+ *   cu_seqlens  [num_seqs + 1] int32 (cu_seqlens_is_int64 == 0) or int64, naturally aligned;
  *               values are clamped into [0, total_tokens] and a decreasing pair
  *               is treated as an empty sequence, so no access leaves the buffers
  *   scale       0 selects 1/sqrt(128)
- *   output      [total_tokens, 8, 128] bf16 (written; rows outside every sequence untouched)
+ *   output      [total_tokens, 8, 128] bf16 (written, 8-byte aligned; rows outside every sequence untouched)
  *   new_state   [num_seqs, 8, 128, 128] fp32 (written; 16-byte aligned; must not be `state`)
  *   workspace   device scratch of at least gdn_prefill_workspace_bytes() bytes, 256-byte aligned
  */

@@ -23,6 +23,9 @@ INCLUDE_DIR = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libgdn_mi355x.so"
 SOURCES = ("gdn_decode.hip", "gdn_prefill.hip", "gdn_capi.hip")
+# bandwidth probe for bench.py (measurement only, not an entry point of the path)
+PROBE_PATH = LIB_DIR / "libhbm_probe.so"
+PROBE_SOURCES = ("hbm_stream.hip",)
 ARCH = "gfx950"
 
 # Every HIP translation unit is built with packed-fp32 instructions disabled.
@@ -53,24 +56,30 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found; the gfx950 library cannot be built")
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile the HIP sources into LIB_PATH (atomic replace)."""
+def _compile(sources, target: Path, verbose: bool) -> Path:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    fd, tmp = tempfile.mkstemp(prefix="libgdn_mi355x.", suffix=".so.tmp", dir=LIB_DIR)
+    fd, tmp = tempfile.mkstemp(prefix=target.stem + ".", suffix=".so.tmp", dir=LIB_DIR)
     os.close(fd)
     cmd = [hipcc_path(), *HIPCC_FLAGS, f"-I{INCLUDE_DIR}", "-o", tmp,
-           *[str(CSRC_DIR / s) for s in SOURCES]]
+           *[str(CSRC_DIR / s) for s in sources]]
     try:
         res = subprocess.run(cmd, capture_output=True, text=True)
         if res.returncode != 0:
             raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
         if verbose:
             print(" ".join(cmd))
-        os.replace(tmp, LIB_PATH)
+        os.replace(tmp, target)
     finally:
         if os.path.exists(tmp):
             os.unlink(tmp)
-    return LIB_PATH
+    return target
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile the HIP sources into LIB_PATH and the bandwidth probe into
+    PROBE_PATH (atomic replace of each)."""
+    _compile(PROBE_SOURCES, PROBE_PATH, verbose)
+    return _compile(SOURCES, LIB_PATH, verbose)
 
 
 _LIB = None
@@ -96,6 +105,23 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
     _LIB = lib
     return lib
+
+
+_PROBE = None
+
+
+def load_probe() -> ctypes.CDLL:
+    """The bandwidth probe library (bench.py only)."""
+    global _PROBE
+    if _PROBE is None:
+        if not PROBE_PATH.exists():
+            raise RuntimeError(f"{PROBE_PATH} is missing: run build() first")
+        import torch  # noqa: F401
+        lib = ctypes.CDLL(str(PROBE_PATH))
+        lib.hbm_stream_copy.restype = ctypes.c_int
+        lib.hbm_stream_copy.argtypes = [_VP, _VP, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, _VP]
+        _PROBE = lib
+    return _PROBE
 
 
 def check(status: int, what: str) -> None:

@@ -142,6 +142,11 @@ extern "C" int gdn_decode_fwd(const void* q, const void* k, const void* v, const
     return GDN_ERR_UNALIGNED;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 7u)
     return GDN_ERR_UNALIGNED;
+  // v, a, b, out: 2-byte accesses; A_log, dt_bias: 4-byte
+  if ((reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) |
+       reinterpret_cast<uintptr_t>(out)) & 1u)
+    return GDN_ERR_UNALIGNED;
+  if ((reinterpret_cast<uintptr_t>(A_log) | reinterpret_cast<uintptr_t>(dt_bias)) & 3u) return GDN_ERR_UNALIGNED;
   if (state == new_state) return GDN_ERR_ALIASING;
   if (!(scale > 0.0f) && !(scale < 0.0f)) scale = 0.08838834764831845f;  // 0 / NaN -> 1/sqrt(128)
   if (rows_per_wave == 0) rows_per_wave = (batch >= 16) ? 32 : 16;

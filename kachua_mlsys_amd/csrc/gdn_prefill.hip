@@ -48,7 +48,7 @@
 namespace gdn {
 
 constexpr int kChunk = 64;
-constexpr int kFragElems = 4096;             // 64x64 16-bit operand in fragment order
+constexpr int kFragTile = 512;               // one 16x32 MFMA operand fragment: 64 lanes x 8 16-bit values
 // Gate block per (record, v-head): gam[64], tail[64], the chunk's map bound
 // (below) at [128], padding to 256 floats (one 1 KB copy).
 constexpr int kGamStride = 4 * kChunk;
@@ -78,6 +78,14 @@ __host__ __device__ constexpr int perm_depth(int d, int lg, int s) {
   return 32 * d + 16 * (s >> 2) + 4 * lg + (s & 3);
 }
 
+// Tb and Aqk are lower triangular, so fragments (m, d) = (0, 1) and (1, 1)
+// (rows 0-31, columns 32-63) are zero.  Only the other six are stored, copied
+// and multiplied: fragment (m, d) sits at slot frag_slot(m, d) of a matrix of
+// kMatElems values.
+__host__ __device__ constexpr bool frag_zero(int m, int d) { return m < 2 && d == 1; }
+__host__ __device__ constexpr int frag_slot(int m, int d) { return m < 2 ? m : 2 * m - 2 + d; }
+constexpr int kMatFrags = 6;
+constexpr int kMatElems = kMatFrags * kFragTile;   // one packed 64x64 matrix
 // ---- segments ---------------------------------------------------------------
 // A long sequence is cut into segments of L chunks (L chosen per call by the
 // planner).  Segment 0 runs from the true initial state.  Segment j >= 1 runs
@@ -179,7 +187,7 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   const size_t G = static_cast<size_t>(max_segments(tokens));
   const size_t N = static_cast<size_t>(num_seqs);
   size_t off = 0;
-  L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kFragElems * sizeof(uint16_t));
+  L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kMatElems * sizeof(uint16_t));
   L.gam_off = off;   off = align256(off + R * kVHeads * kGamStride * sizeof(float));
   L.start_off = off; off = align256(off + (N + 1) * sizeof(int));
   L.list_off = off;  off = align256(off + list_ints(num_seqs, static_cast<long long>(G)) * sizeof(int));
@@ -856,7 +864,7 @@ __global__ __launch_bounds__(kPrepassThreads, 4) void prepass_kernel(
   uint16_t* frag2[kGva];
 #pragma unroll
   for (int e = 0; e < kGva; ++e)
-    frag2[e] = ws_frag + (static_cast<size_t>(r) * kVHeads + kGva * hq + e) * kFrags * kFragElems;
+    frag2[e] = ws_frag + (static_cast<size_t>(r) * kVHeads + kGva * hq + e) * kFrags * kMatElems;
   const int rsw = kq_swz(l16);
   f32x4 akk[2], aqk[2];
 #pragma unroll
@@ -911,18 +919,17 @@ __global__ __launch_bounds__(kPrepassThreads, 4) void prepass_kernel(
           const int i = 16 * ni + 4 * lg + rr;
           x[rr] = i <= t ? fast_exp2(gt - gi4[rr]) * aqk[n][rr] : 0.0f;
         }
-        *reinterpret_cast<u32x2*>(frag2[e] + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + lane) * 8 + 4 * (ni & 1)) =
+        *reinterpret_cast<u32x2*>(frag2[e] + kMatElems + (frag_slot(mi, ni >> 1) * 64 + lane) * 8 + 4 * (ni & 1)) =
             u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
       }
     }
   }
-  // the six half-fragments of Aqk above the diagonal, both v-heads: (mi, ni) =
-  // (0,1) (0,2) (0,3) (1,2) (1,3) (2,3)
-  for (int z = tid; z < kGva * 6 * 64; z += kPrepassThreads) {
-    const int e = z / (6 * 64), zj = (z >> 6) % 6, zl = z & 63;
-    const int mi = zj < 3 ? 0 : (zj < 5 ? 1 : 2);
-    const int ni = zj < 3 ? zj + 1 : (zj < 5 ? zj - 1 : 3);
-    *reinterpret_cast<u32x2*>(frag2[e] + kFragElems + ((mi * 2 + (ni >> 1)) * 64 + zl) * 8 + 4 * (ni & 1)) =
+  // the stored half-fragments of Aqk above the diagonal, both v-heads: tiles
+  // (mi, ni) = (0, 1) in fragment (0, 0) and (2, 3) in fragment (2, 1)
+  if (tid < kGva * 2 * 64) {
+    const int e = tid >> 7, zl = tid & 63;
+    const int mi = (tid & 64) ? 2 : 0, ni = mi + 1;
+    *reinterpret_cast<u32x2*>(frag2[e] + kMatElems + (frag_slot(mi, ni >> 1) * 64 + zl) * 8 + 4 * (ni & 1)) =
         u32x2{0u, 0u};
   }
   __syncthreads();   // N complete; K / Q space becomes T
@@ -976,9 +983,10 @@ __global__ __launch_bounds__(kPrepassThreads, 4) void prepass_kernel(
   __syncthreads();
 
   // ---- pack Tb = T diag(beta) as fp16 (permuted fragment order), per v-head ----
-  // fragment (m, d), lane l: row t = 16 m + l % 16, slots s: i = perm_depth(d, l / 16, s)
-  for (int qi = tid & 255; qi < 512; qi += 256) {
-    const int m = qi >> 7, d = (qi >> 6) & 1, l = qi & 63;
+  // fragment (m, d) at slot f, lane l: row t = 16 m + l % 16, slots s: i = perm_depth(d, l / 16, s)
+  for (int qi = tid & 255; qi < kMatFrags * 64; qi += 256) {
+    const int f = qi >> 6, l = qi & 63;
+    const int m = f < 2 ? f : 2 + ((f - 2) >> 1), d = f < 2 ? 0 : (f & 1);
     const int t = 16 * m + (l & 15);
     const int i0 = 32 * d + 4 * (l >> 4);
     const int e = tid >> 8;
@@ -1025,7 +1033,7 @@ struct __align__(16) ConsumerSmem {
   uint16_t ks[2][kChunk][kDim];
   uint16_t qs[2][kChunk][kDim];
   uint16_t vs[2][kChunk][kDim];
-  uint16_t frag[2][kFrags][kFragElems];
+  uint16_t frag[2][kFrags][kMatElems];
   float gt[2][4 * kChunk];
 };
 
@@ -1104,10 +1112,14 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
     dma16<2>(vb + row * (kVHeads * kDim * 2) + dl.v_col, &sm.vs[P][32 * j + 4 * w][0]);   // read once
   }
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
-  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * kFrags * kFragElems);
-#pragma unroll
-  for (int j = 0; j < kFrags; ++j)
-    dma16<2>(fb + (512 * j + 64 * w + lane) * 16, &sm.frag[P][0][0] + (512 * j + 64 * w) * 8);   // read once
+  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * kFrags * kMatElems);
+  // 12 fragments of 1 KB (Tb then Aqk, contiguous here and in LDS): wave w
+  // copies w and w + 8; waves 4-7 copy their first fragment again (the same
+  // bytes to the same place: branch-free, which keeps this path spill-free)
+  static_assert(kFrags * kMatFrags == 12, "fragment copy split");
+  const int w2 = w < 4 ? w + 8 : w;
+  dma16<2>(fb + (64 * w + lane) * 16, &sm.frag[P][0][0] + 64 * w * 8);   // read once
+  dma16<2>(fb + (64 * w2 + lane) * 16, &sm.frag[P][0][0] + 64 * w2 * 8);
   if (w == 0)   // gam, tail and the map bound: one 1 KB block
     dma16(reinterpret_cast<const char*>(ws_gam + rh * kGamStride) + 16 * lane, &sm.gt[P][0]);
 }
@@ -1181,7 +1193,8 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
     D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 2; ++d)
-      D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][((m * 2 + d) * 64 + lane) * 8]), rf[d], D[m]);
+      if (!frag_zero(m, d))
+        D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][(frag_slot(m, d) * 64 + lane) * 8]), rf[d], D[m]);
   }
 
   // ---- Delta as bf16 (output) and Delta' = tail Delta as hi + lo (state) ----
@@ -1208,7 +1221,8 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
     f32x4 OT = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 0; d < 2; ++d)
-      OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][((m * 2 + d) * 64 + lane) * 8]), OT);
+      if (!frag_zero(m, d))
+        OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][(frag_slot(m, d) * 64 + lane) * 8]), OT);
     const int t = 16 * m + l16;
     const float sg = scale * sm.gt[P][t];
     const u32x2 pk = {pack_bf2(sg * YT[m][0] + scale * OT[0], sg * YT[m][1] + scale * OT[1]),
@@ -1393,7 +1407,7 @@ struct __align__(16) SplitSmem {
   uint16_t ks[2][kChunk][kDim];
   uint16_t qs[2][kChunk][kDim];
   uint16_t vs[2][kChunk][kHalfV];          // this half's value columns; chunk j of row t at j ^ vh_swz(t)
-  uint16_t frag[2][kFrags][kFragElems];
+  uint16_t frag[2][kFrags][kMatElems];
   float gt[2][4 * kChunk];
   u32x4 sbx[4][4][64];                     // chain wave w: bf16 S fragments sb[d], per lane
   u32x4 dox[4][2][64];                     // chain wave w: bf16 Delta fragments dob[d], per lane
@@ -1465,9 +1479,11 @@ __device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, con
 #pragma unroll
   for (int j = 0; j < 2; ++j) dma16_buf<2>(vr, dl.v[j], &sm.vs[P][32 * j + 8 * ws][0]);   // V: read once
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
-  const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kFrags * kFragElems, kFrags * kFragElems * 2);
+  // 12 fragments of 1 KB (Tb then Aqk): side wave ws copies ws, ws + 4, ws + 8
+  const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kFrags * kMatElems, kFrags * kMatElems * 2);
 #pragma unroll
-  for (int j = 0; j < 2 * kFrags; ++j) dma16_buf(fr, dl.fr + 4096u * j, &sm.frag[P][0][0] + (256 * j + 64 * ws) * 8);
+  for (int j = 0; j < kFrags * kMatFrags / 4; ++j)
+    dma16_buf(fr, dl.fr + 4096u * j, &sm.frag[P][0][0] + (256 * j + 64 * ws) * 8);
   if (ws == 0) dma16_buf(buf_rsrc(ws_gam + rh * kGamStride, kGamStride * 4), dl.g, &sm.gt[P][0]);
 }
 
@@ -1526,7 +1542,7 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   for (int d = 0; d < 2; ++d)
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-      tb[d][m] = *reinterpret_cast<const f16x8*>(&sm.frag[P][0][((m * 2 + d) * 64 + lane) * 8]);
+      if (!frag_zero(m, d)) tb[d][m] = *reinterpret_cast<const f16x8*>(&sm.frag[P][0][(frag_slot(m, d) * 64 + lane) * 8]);
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- R = V - gam X, Delta = Tb R (fp16) ----
@@ -1550,7 +1566,8 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
 #pragma unroll
   for (int d = 0; d < 2; ++d)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) D[m] = mfma16h(tb[d][m], rf[d], D[m]);
+    for (int m = 0; m < 4; ++m)
+      if (!frag_zero(m, d)) D[m] = mfma16h(tb[d][m], rf[d], D[m]);
 
   // operands of the state update, read while Delta forms: tail gates and the
   // K^T fragments (tile kt, row i of the A operand is k = kappa(kt, i/4, i%4);
@@ -1642,7 +1659,7 @@ __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, floa
   for (int m = 0; m < 4; ++m) {
 #pragma unroll
     for (int d = 0; d < 2; ++d)
-      fa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][((m * 2 + d) * 64 + lane) * 8]);
+      if (!frag_zero(m, d)) fa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][(frag_slot(m, d) * 64 + lane) * 8]);
     sg[m] = scale * sm.gt[P][16 * m + l16];
   }
   lds_barrier();   // B2
@@ -1656,7 +1673,8 @@ __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, floa
 #pragma unroll
   for (int d = 0; d < 2; ++d)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) OT[m] = mfma16(dob[d], fa[d][m], OT[m]);
+    for (int m = 0; m < 4; ++m)
+      if (!frag_zero(m, d)) OT[m] = mfma16(dob[d], fa[d][m], OT[m]);
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const int t = 16 * m + l16;
@@ -2190,9 +2208,16 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (!cu_seqlens || !new_state || !workspace || !A_log || !dt_bias)
     return GDN_ERR_INVALID_ARGUMENT;
   if (total_tokens > 0 && (!q || !k || !v || !a || !b || !output)) return GDN_ERR_INVALID_ARGUMENT;
-  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k)) & 15u) return GDN_ERR_UNALIGNED;
+  // q, k, v: 16-byte copies straight into LDS; output: 8-byte stores; states:
+  // 16-byte accesses; a, b: 2-byte loads; cu_seqlens: 4- or 8-byte loads
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15u)
+    return GDN_ERR_UNALIGNED;
+  if (reinterpret_cast<uintptr_t>(output) & 7u) return GDN_ERR_UNALIGNED;
+  if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b)) & 1u) return GDN_ERR_UNALIGNED;
+  if (reinterpret_cast<uintptr_t>(cu_seqlens) & (cu_seqlens_is_int64 ? 7u : 3u)) return GDN_ERR_UNALIGNED;
   if ((reinterpret_cast<uintptr_t>(state) | reinterpret_cast<uintptr_t>(new_state)) & 15u)
     return GDN_ERR_UNALIGNED;
+  if ((reinterpret_cast<uintptr_t>(A_log) | reinterpret_cast<uintptr_t>(dt_bias)) & 3u) return GDN_ERR_UNALIGNED;
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
   if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
   const long long R = max_records(num_seqs, total_tokens);

@@ -65,6 +65,9 @@ def test_c_decode_rejects_before_launch(lib):
     assert f(*args, 0.0, A16, A16b, 0, 0, NULL) == 0                       # empty batch: no-op
     bad = list(args); bad[3] = A16 + 4                                      # state not 16B aligned
     assert f(*bad, 0.0, A16, A16b, 1, 0, NULL) == -3
+    bad = list(args); bad[2] = A16 + 1                                      # v not 2B aligned
+    assert f(*bad, 0.0, A16, A16b, 1, 0, NULL) == -3
+    assert f(*args, 0.0, A16 + 1, A16b, 1, 0, NULL) == -3                  # out not 2B aligned
     same = list(args); same[3] = A16b                                       # state == new_state
     assert f(*same, 0.0, A16, A16b, 1, 0, NULL) == -4
     assert f(*args, 0.0, A16, A16b, 1, 8, NULL) == -1                      # bad rows_per_wave
@@ -84,6 +87,14 @@ def test_c_prefill_rejects_before_launch(lib):
     x = list(base); x[15] = A16 + 16                                        # workspace not 256B aligned
     assert f(*x) == -3
     x = list(base); x[0] = A16 + 8                                          # q not 16B aligned
+    assert f(*x) == -3
+    x = list(base); x[2] = A16 + 8                                          # v not 16B aligned
+    assert f(*x) == -3
+    x = list(base); x[13] = A16 + 4                                         # output not 8B aligned
+    assert f(*x) == -3
+    x = list(base); x[7] = A16 + 1                                          # b not 2B aligned
+    assert f(*x) == -3
+    x = list(base); x[9] = 1; x[8] = A16 + 4                                # int64 cu_seqlens not 8B aligned
     assert f(*x) == -3
     x = list(base); x[3] = A16b                                             # state aliases new_state
     assert f(*x) == -4
