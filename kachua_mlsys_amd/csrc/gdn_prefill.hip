@@ -695,61 +695,256 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // ============================================================================
-// prepass: chunk-local WY terms for one (record, v-head)
+// prepass: chunk-local WY terms, one wave per item
 // ============================================================================
-constexpr int kPrepassThreads = 512;   // 8 waves: waves 0-3 serve v-head 2hq, waves 4-7 v-head 2hq+1
-constexpr int kMRow = 68;     // floats per LDS row of the 64x64 fp32 matrices (16-byte aligned)
+// Each wave runs whole items on its own, with no work-group barrier: the K / Q
+// rows come straight from global memory into MFMA operand registers (16 bytes
+// of a row per lane is both the A and the B fragment of a gram), the gates sit
+// on the lanes (lane = token), and only the 16x16 diagonal blocks of the
+// triangular inverse pass through LDS.  Two waves per SIMD are resident
+// (kPrepassResident in all).  An item is one (record, v-head) when the batch
+// has at most that many, else one (record, q/k head) whose wave forms the
+// grams once and then runs both v-heads of the GVA pair, so every item of a
+// batch of up to 512 records starts at once.
+//
+// The inverse is formed transposed: with U = I + N^T (unit upper) and
+// W = U^{-1} = T^T, the 16x16 blocks satisfy
+//   W_aa = (T_aa)^T,   W_ab = -W_aa sum_{m=a+1..b} U_am W_mb   (a < b),
+// T_aa by forward substitution (one lane per column), the off-diagonal blocks
+// on MFMA.  W in MFMA C layout holds Tb^T = diag(beta) W with lane = row of
+// Tb, which is exactly the register order of Tb's A fragments.
+constexpr int kPrepassThreads = 256;              // four independent waves
+constexpr int kPrepassWaves = kPrepassThreads / 64;
+constexpr int kPrepassMaxGroups = 512;             // two per CU: eight waves, two per SIMD
+constexpr int kPrepassResident = kPrepassMaxGroups * kPrepassWaves;
 
-// 71.2 KB: two work-groups (four v-heads' worth) per CU.  The T matrices reuse
-// the K / Q rows' space once the grams have been formed.
-struct __align__(16) PrepassSmem {
-  union {
-    uint16_t kq[2][kChunk][kDim];   // K, Q rows (bf16, chunk-swizzled)
-    float tm[kGva][kChunk][kMRow];  // T = (I + N)^{-1} per v-head of the pair
-  } u;
-  float nm[kGva][kChunk][kMRow];    // N = strict lower beta_t rho K K^T (before it: the record search's scratch)
-  float lgam[kGva][kChunk];         // Gam_t / ln 2 (log2 cumulative decay)
+struct __align__(16) PrepassWaveSmem {   // per v-head of the item
+  float lgam[kGva][kChunk];    // Gam_t / ln 2 (inclusive scan of log2 g)
   float beta[kGva][kChunk];
-  float kb2[kGva][kChunk];          // log2 max(1, |1 - beta_t |k_t|^2|)
+  float nd[kGva][4][16][16];   // diagonal blocks N_aa, column-major: nd[a][column][row]
+  float td[kGva][4][16][16];   // their inverses T_aa, column-major
 };
 
-// j-th lower 16x16 tile (mi >= ni) of a 4x4 tile grid, row by row:
-// (0,0) (1,0) (1,1) (2,0) (2,1) (2,2) (3,0) (3,1) (3,2) (3,3).
-__device__ __forceinline__ void lower_tile(int j, int& mi, int& ni) {
-  mi = j >= 6 ? 3 : (j >= 3 ? 2 : (j >= 1 ? 1 : 0));
-  ni = j - mi * (mi + 1) / 2;
-}
+union PrepassSmem {
+  PrepassWaveSmem w[kPrepassWaves];
+  int plan[kPlanScratch];      // planner scratch (work-group 0 of a fused launch)
+};
 
-// acc += X Y for 16x16 fp32 blocks in LDS (row stride kMRow) on fp32 MFMA;
-// result in C layout (lane (lg, l16) holds rows 4 lg .. 4 lg + 3 of column l16).
-__device__ __forceinline__ f32x4 block_prod(f32x4 acc, const float* X, const float* Y, int l16, int lg) {
-#pragma unroll
-  for (int kc = 0; kc < 4; ++kc)
-    acc = mfma_f32(X[l16 * kMRow + 4 * kc + lg], Y[(4 * kc + lg) * kMRow + l16], acc);
+// Batches of at most kFusedPlanSeqs sequences number their records inside the
+// prepass (no plan launch): every wave scans the chunk counts of all sequences
+// once (64 per lane block) and finds each item's sequence with a ballot.
+constexpr int kFusedPlanSeqs = 512;
+constexpr int kFusedBlocks = kFusedPlanSeqs / 64;
+
+// acc + X Y for 16x16 fp32 blocks with X^T and Y in C layout (lane (lg, l16),
+// register r: row 4 lg + r, column l16), on two bf16 MFMAs with both operands
+// split into bf16 hi + lo: X_hi Y_hi + X_lo Y_hi + X_hi Y_lo (relative error
+// about 2^-16, far below the fp16 rounding of Tb).  Depth slot s of lane group
+// lg is product depth 4 lg + (s & 3): slots 0-3 pair X_hi with Y_hi, slots 4-7
+// X_lo with Y_hi in the first MFMA and X_hi with Y_lo... as 0 x lo in the
+// second, where slots 4-7 of B are zero.
+__device__ __forceinline__ f32x4 prod16(const f32x4& xt, const f32x4& y, f32x4 acc) {
+  const uint32_t xh0 = pack_bf2(xt[0], xt[1]), xh1 = pack_bf2(xt[2], xt[3]);
+  const uint32_t xl0 = pack_bf2(xt[0] - bf_lo(xh0), xt[1] - bf_hi(xh0));
+  const uint32_t xl1 = pack_bf2(xt[2] - bf_lo(xh1), xt[3] - bf_hi(xh1));
+  const uint32_t yh0 = pack_bf2(y[0], y[1]), yh1 = pack_bf2(y[2], y[3]);
+  const uint32_t yl0 = pack_bf2(y[0] - bf_lo(yh0), y[1] - bf_hi(yh0));
+  const uint32_t yl1 = pack_bf2(y[2] - bf_lo(yh1), y[3] - bf_hi(yh1));
+  const bf16x8 xa = __builtin_bit_cast(bf16x8, u32x4{xh0, xh1, xl0, xl1});
+  acc = mfma16(xa, __builtin_bit_cast(bf16x8, u32x4{yh0, yh1, yh0, yh1}), acc);
+  acc = mfma16(xa, __builtin_bit_cast(bf16x8, u32x4{yl0, yl1, 0u, 0u}), acc);
   return acc;
 }
 
-__device__ __forceinline__ void block_store(float* Z, const f32x4& v, float sc, int l16, int lg) {
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) Z[(4 * lg + rr) * kMRow + l16] = sc * v[rr];
+// Wave-local LDS hand-off between lanes of one wave: LDS operations of a wave
+// complete in order; this keeps the compiler from moving them across.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Batches of at most kFusedPlanSeqs sequences number their records inside the
-// prepass (no plan launch): thread s owns sequence s, and an exclusive scan of
-// the chunk counts gives each sequence's first record.
-constexpr int kFusedPlanSeqs = kPrepassThreads;
-static_assert(kPlanScratch <= kGva * kChunk * kMRow, "planner scratch must fit in N's space");
+// The terms of NH v-heads (one, or both of a GVA pair, interleaved phase by
+// phase so that their independent latency chains overlap) from the chunk's raw
+// grams: kk[m][n] (n <= m) holds [t = 16 m + 4 lg + rr][i = 16 n + l16] =
+// k_t . k_i; qk[a][m] (a <= m) holds [i = 16 a + 4 lg + rr][t = 16 m + l16] =
+// k_i . q_t.  a_t, b_t: this lane's token (clamped into the chunk) per v-head.
+template <int NH>
+__device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4], const f32x4 (&qk)[4][4],
+                                              int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
+                                              const float (&alog)[kGva], const float (&dtb)[kGva],
+                                              uint16_t* __restrict__ frag0, float* __restrict__ gp0) {
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  // per-head workspace blocks are consecutive v-heads of one record
+  constexpr size_t kFragStride = static_cast<size_t>(kFrags) * kMatElems;
 
-// At most this many prepass work-groups (two per CU); the grid never needs a
-// third round: the first work-groups, dispatched first, take a second item.
-constexpr int kPrepassGroups = 2 * 256;
-constexpr int kPrepassMaxGrid = 2 * kPrepassGroups;
+  // ---- gates: Gam_t = inclusive scan of log2 g (clamped: g = e^-100 is
+  // already 0 to fp32 working precision, and a finite floor keeps Gam
+  // finite), beta_t; gam / tail to the workspace ----
+  float last[NH];
+#pragma unroll
+  for (int e = 0; e < NH; ++e) {
+    const float lgv = lane < c ? fmaxf(log_decay(alog[e], a_t[e], dtb[e]), -100.0f) * kLog2e : 0.0f;
+    const float bet = lane < c ? sigmoidf(b_t[e]) : 0.0f;
+    const float lgam = wave_incl_sumf(lgv);
+    last[e] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lgam), c - 1));
+    float* gp = gp0 + e * kGamStride;
+    gp[lane] = lane < c ? fast_exp2(lgam) : 0.0f;
+    gp[kChunk + lane] = lane < c ? fast_exp2(last[e] - lgam) : 0.0f;
+    ws.lgam[e][lane] = lgam;
+    ws.beta[e][lane] = bet;
+  }
+  wave_lds_sync();
+  float lcol[NH][4];     // Gam at column 16 n + l16
+  f32x4 lrow[NH][4];     // Gam at rows 16 m + 4 lg + rr
+  f32x4 brow[NH][4];     // beta at rows 16 m + 4 lg + rr
+#pragma unroll
+  for (int e = 0; e < NH; ++e)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      lcol[e][m] = ws.lgam[e][16 * m + l16];
+      lrow[e][m] = *reinterpret_cast<const f32x4*>(&ws.lgam[e][16 * m + 4 * lg]);
+      brow[e][m] = *reinterpret_cast<const f32x4*>(&ws.beta[e][16 * m + 4 * lg]);
+    }
 
-// Items (record, q/k head), item i = 4 r + hq; work-group wg takes items
-// wg, wg + nwg, ...  For each item the K / Q rows and both grams are shared by
-// the two v-heads of the GVA pair; gates, weighting, inverse and packing run
-// per v-head on waves 0-3 / 4-7.
-__global__ __launch_bounds__(kPrepassThreads, 4) void prepass_kernel(
+  // ---- Aqk = lower(rho . Q K^T), formed transposed: tile (a, m) holds slots
+  // 4 (a & 1) .. + 3 of Aqk fragment (m, a >> 1) ----
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      if (frag_zero(m, d)) continue;
+#pragma unroll
+      for (int e = 0; e < NH; ++e) {
+        float x[8];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int ai = 2 * d + hf;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int i = 16 * ai + 4 * lg + rr, t = 16 * m + l16;
+            x[4 * hf + rr] = (ai <= m && i <= t) ? fast_exp2(lcol[e][m] - lrow[e][ai][rr]) * qk[ai][m][rr] : 0.0f;
+          }
+        }
+        *reinterpret_cast<u32x4*>(frag0 + e * kFragStride + kMatElems + (frag_slot(m, d) * 64 + lane) * 8) =
+            u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])};
+      }
+    }
+  }
+
+  // ---- N = strict_lower(beta_t rho K K^T): diagonal tiles to LDS
+  // (column-major) for the substitution, their diagonal |k_t|^2 into the
+  // chunk's map bound; lower tiles stay in registers ----
+  f32x4 nlo[NH][4][4];     // nlo[e][m][n], n < m
+  float kb[NH];            // log2 max(1, |1 - beta_t |k_t|^2|) of the token this lane holds (else 0)
+#pragma unroll
+  for (int e = 0; e < NH; ++e) {
+    kb[e] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int n = 0; n <= m; ++n) {
+        f32x4 nv;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int t = 16 * m + 4 * lg + rr, i = 16 * n + l16;
+          nv[rr] = i < t ? brow[e][m][rr] * fast_exp2(lrow[e][m][rr] - lcol[e][n]) * kk[m][n][rr] : 0.0f;
+        }
+        if (n == m) {
+          // t = 16 m + l16 sits on the lane whose rows include it (rr = l16 - 4 lg);
+          // rows t >= c have beta = 0 and contribute 0
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (l16 == 4 * lg + rr) kb[e] += __log2f(fmaxf(1.0f, fabsf(1.0f - brow[e][m][rr] * kk[m][m][rr])));
+          *reinterpret_cast<f32x4*>(&ws.nd[e][m][l16][4 * lg]) = nv;
+        } else {
+          nlo[e][m][n] = nv;
+        }
+      }
+    }
+  }
+  wave_lds_sync();
+
+  // ---- T_aa = (I + N_aa)^{-1} by forward substitution: lane (a = lg, j = l16)
+  // forms column j of T_aa; once x[i] is final every later row subtracts
+  // N[r][i] x[i] (the row-wise recurrence's terms and order, dependency depth 16) ----
+#pragma unroll
+  for (int e = 0; e < NH; ++e) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = i == l16 ? 1.0f : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 15; ++i) {
+      float col[16];
+#pragma unroll
+      for (int qv = (i + 1) >> 2; qv < 4; ++qv) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(&ws.nd[e][lg][i][4 * qv]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) col[4 * qv + u] = v4[u];
+      }
+#pragma unroll
+      for (int rr = i + 1; rr < 16; ++rr) x[rr] = fmaf(-col[rr], x[i], x[rr]);
+    }
+#pragma unroll
+    for (int qv = 0; qv < 4; ++qv)
+      *reinterpret_cast<f32x4*>(&ws.td[e][lg][l16][4 * qv]) = f32x4{x[4 * qv], x[4 * qv + 1], x[4 * qv + 2], x[4 * qv + 3]};
+  }
+  wave_lds_sync();
+
+  // ---- W = T^T: diagonal blocks from LDS in both orientations, the
+  // off-diagonal blocks by distance, then Tb^T = diag(beta) W (row i = 16 a +
+  // 4 lg + rr) as fp16 fragments: fragment (m, d) slots 0-3 from tile (2 d, m),
+  // slots 4-7 from (2 d + 1, m).  One v-head after the other (registers). ----
+#pragma unroll
+  for (int e = 0; e < NH; ++e) {
+    f32x4 tc[4], w[4][4];   // tc[a] = T_aa = (W_aa)^T in C layout; w[a][b] = W_ab, a <= b
+#pragma unroll
+    for (int ab = 0; ab < 4; ++ab) {
+      tc[ab] = *reinterpret_cast<const f32x4*>(&ws.td[e][ab][l16][4 * lg]);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) w[ab][ab][rr] = ws.td[e][ab][4 * lg + rr][l16];
+    }
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dist = 1; dist < 4; ++dist) {
+#pragma unroll
+      for (int ab = 0; ab + dist < 4; ++ab) {
+        const int bb = ab + dist;
+        // P = sum_m U_am W_mb with U_am^T = N_ma (C layout)
+        f32x4 p = prod16(nlo[e][ab + 1][ab], w[ab + 1][bb], z4);
+        if (dist >= 2) p = prod16(nlo[e][ab + 2][ab], w[ab + 2][bb], p);
+        if (dist >= 3) p = prod16(nlo[e][ab + 3][ab], w[ab + 3][bb], p);
+        w[ab][bb] = -prod16(tc[ab], p, z4);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+#pragma unroll
+      for (int d = 0; d < 2; ++d) {
+        if (frag_zero(m, d)) continue;
+        float x[8];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          const int ai = 2 * d + hf;
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = ai <= m ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
+        }
+        *reinterpret_cast<u32x4*>(frag0 + e * kFragStride + (frag_slot(m, d) * 64 + lane) * 8) =
+            u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
+      }
+    }
+  }
+
+  // the chunk's map bound: sum over tokens of log2 g_t + log2 max(1, |1 - beta_t |k_t|^2|)
+#pragma unroll
+  for (int e = 0; e < NH; ++e) {
+    const float lb = wave_sumf(kb[e]) + last[e];
+    if (lane == 0) gp0[e * kGamStride + kBoundAt] = lb;
+  }
+}
+
+__global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
@@ -757,258 +952,157 @@ __global__ __launch_bounds__(kPrepassThreads, 4) void prepass_kernel(
     int gcap, int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
     uint16_t* __restrict__ ws_frag, float* __restrict__ ws_gam) {
   __shared__ PrepassSmem sm;
-  int* scratch = reinterpret_cast<int*>(&sm.nm[0][0][0]);   // N's space until the grams
   if (fused_plan && blockIdx.x == 0) {
     // work-group 0 plans the batch (lists for the consumer) while the others
     // run the records
     int total_recs;
-    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, scratch, total_recs);
+    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, sm.plan, total_recs);
     return;
   }
-  const int wg = static_cast<int>(blockIdx.x) - fused_plan;
-  const int nwg = static_cast<int>(gridDim.x) - fused_plan;
-  // records: small batches scan the chunk counts here (thread s owns sequence s)
-  long long st0 = 0, st1 = 0;
-  int sbase = 0, snch = 0, total;
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+  PrepassWaveSmem& ws = sm.w[wv];
+  const int gw = (static_cast<int>(blockIdx.x) - fused_plan) * kPrepassWaves + wv;
+  const int nw = (static_cast<int>(gridDim.x) - fused_plan) * kPrepassWaves;
+
+  // records: small batches scan the chunk counts here (lane l of block j owns
+  // sequence 64 j + l); incl = inclusive prefix of the chunk counts.  The
+  // bounds of block 0's sequences stay in registers.
+  int incl[kFusedBlocks];
+  long long b0s0 = 0, b0s1 = 0;
+  int total;
   if (fused_plan) {
-    if (static_cast<int>(threadIdx.x) < num_seqs) seq_bounds(cu, is64, threadIdx.x, T, st0, st1);
-    snch = static_cast<int>((st1 - st0 + kChunk - 1) / kChunk);
-    const int inc = block_scan<kPrepassThreads>(snch, scratch + 16);
-    sbase = inc - snch;
-    if (threadIdx.x == kPrepassThreads - 1) scratch[8] = inc;
-    __syncthreads();
-    total = min(scratch[8], R);
+    int carry = 0;
+#pragma unroll
+    for (int j = 0; j < kFusedBlocks; ++j) {
+      int nch = 0;
+      if (64 * j < num_seqs) {
+        const int s = 64 * j + lane;
+        if (s < num_seqs) {
+          long long t0, t1;
+          seq_bounds(cu, is64, s, T, t0, t1);
+          nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+          if (j == 0) {
+            b0s0 = t0;
+            b0s1 = t1;
+          }
+        }
+        incl[j] = wave_incl_sum(nch) + carry;
+        carry = __builtin_amdgcn_readlane(incl[j], 63);
+      } else {
+        incl[j] = carry;
+      }
+    }
+    total = min(carry, R);
   } else {
     total = min(rec_start[num_seqs], R);
   }
-  for (int item = wg; item < total * kQKHeads; item += nwg) {
-  const int r = item / kQKHeads;
-  const int hq = item % kQKHeads;
-  int c;
-  long long t0;
-  __syncthreads();   // the previous item's readers of T, N, the gates and the scratch are done
-  if (fused_plan) {
-    if (snch > 0 && r >= sbase && r < sbase + snch) {
-      const long long c0 = st0 + static_cast<long long>(r - sbase) * kChunk;
-      scratch[0] = static_cast<int>(min(static_cast<long long>(kChunk), st1 - c0));
-      scratch[2] = static_cast<int>(c0 & 0xffffffffLL);
-      scratch[3] = static_cast<int>(c0 >> 32);
+
+  // items: (record r, v-head h) = 8 r + h, or (record r, q/k head hq) = 4 r + hq
+  // with both v-heads of the pair; consecutive items share a work-group, so the
+  // waves that read the same K / Q rows go through one L2
+  const bool pair_items = static_cast<long long>(total) * kVHeads > kPrepassResident;
+  const int per_rec = pair_items ? kQKHeads : kVHeads;
+  const int nitems = total * per_rec;
+  for (int item = gw; item < nitems; item += nw) {
+    const int r = item / per_rec;
+    const int hq = pair_items ? item % kQKHeads : (item % kVHeads) / kGva;
+    const int e0 = pair_items ? 0 : item % kGva;       // first v-head of the pair this item runs
+    const int ne = pair_items ? kGva : 1;
+    long long t0, s1;
+    if (fused_plan) {
+      int s = 0, start = 0;
+      bool found = false;
+#pragma unroll
+      for (int j = 0; j < kFusedBlocks; ++j) {
+        if (!found && 64 * j < num_seqs) {
+          const unsigned long long m = __builtin_amdgcn_ballot_w64(incl[j] > r);
+          if (m != 0) {
+            const int l = static_cast<int>(__builtin_ctzll(m));
+            s = 64 * j + l;
+            start = l > 0 ? __builtin_amdgcn_readlane(incl[j], l - 1)
+                          : (j > 0 ? __builtin_amdgcn_readlane(incl[j > 0 ? j - 1 : 0], 63) : 0);
+            found = true;
+          }
+        }
+      }
+      long long s0;
+      if (s < 64) {
+        const unsigned long long x0 = static_cast<unsigned long long>(b0s0), x1 = static_cast<unsigned long long>(b0s1);
+        s0 = static_cast<long long>(
+            (static_cast<unsigned long long>(static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x0 >> 32), s))) << 32) |
+            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x0 & 0xffffffffu), s)));
+        s1 = static_cast<long long>(
+            (static_cast<unsigned long long>(static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x1 >> 32), s))) << 32) |
+            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x1 & 0xffffffffu), s)));
+      } else {
+        seq_bounds(cu, is64, s, T, s0, s1);
+      }
+      t0 = s0 + static_cast<long long>(r - start) * kChunk;
+    } else {
+      const int4 rec = recs[r];
+      t0 = rec.y;
+      s1 = t0 + max(rec.z, 1);
     }
-    __syncthreads();
-    c = scratch[0];
-    t0 = static_cast<long long>(static_cast<unsigned>(scratch[2])) | (static_cast<long long>(scratch[3]) << 32);
-    __syncthreads();   // scratch read by every thread before N is written
-  } else {
-    const int4 rec = recs[r];
-    c = max(rec.z, 1);
-    t0 = rec.y;
-  }
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hh = w >> 2;                 // which v-head of the pair this wave serves
-  const int wl = w & 3;                  // wave index within that v-head's group
-  const int h = kGva * hq + hh;
-  const int lane = tid & 63;
-  const int l16 = lane & 15;
-  const int lg = lane >> 4;
+    const int c = static_cast<int>(min(static_cast<long long>(kChunk), s1 - t0));
+    const int cm1 = c - 1;
 
-  // gate inputs first (waves 0 and 4, lane = token): their latency overlaps the row copies
-  float a_t = 0.0f, b_t = 0.0f, alog = 0.0f, dtb = 0.0f;
-  if (wl == 0) {
-    const size_t gi = (t0 + min(lane, c - 1)) * kVHeads + h;
-    a_t = bf2f(a[gi]);
-    b_t = bf2f(b[gi]);
-    alog = A_log[h];
-    dtb = dt_bias[h];
-  }
-
-  // ---- K, Q rows of the chunk, copied straight into LDS ----
-  // Rows past the chunk end repeat row c-1: they meet beta = 0 (rows of N),
-  // i <= t masks (columns) and rows of Aqk whose outputs are never stored.
-  {
-    const size_t qk0 = (static_cast<size_t>(t0) * kQKHeads + hq) * kDim;
-    const char* kb = reinterpret_cast<const char*>(k + qk0);
-    const char* qb = reinterpret_cast<const char*>(q + qk0);
-    const int row0 = 4 * w + (lane >> 4);          // + 32 j keeps row & 15
-    const uint32_t col = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(row0));
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t off = static_cast<uint32_t>(min(row0 + 32 * j, c - 1)) * (kQKHeads * kDim * 2) + col;
-      dma16(kb + off, &sm.u.kq[0][32 * j + 4 * w][0]);
-      dma16(qb + off, &sm.u.kq[1][32 * j + 4 * w][0]);
-    }
-  }
-
-  // ---- gates (waves 0 and 4, lane = token): Gam_t inclusive scan of log2 g, beta ----
-  if (wl == 0) {
-    const int t = lane;
-    // clamp: g = e^-100 is already 0 to fp32 working precision, and a finite
-    // floor keeps Gam finite (no -inf - -inf) for absurd gate inputs
-    const float lgv = t < c ? fmaxf(log_decay(alog, a_t, dtb), -100.0f) * kLog2e : 0.0f;
-    const float bet = t < c ? sigmoidf(b_t) : 0.0f;
-    const float scan = wave_incl_sumf(lgv);
-    sm.lgam[hh][t] = scan;
-    sm.beta[hh][t] = bet;
-    const float last = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scan), c - 1));
-    float* gp = ws_gam + (static_cast<size_t>(r) * kVHeads + h) * kGamStride;
-    gp[t] = t < c ? fast_exp2(scan) : 0.0f;
-    gp[kChunk + t] = t < c ? fast_exp2(last - scan) : 0.0f;
-  }
-  __syncthreads();
-
-  // ---- grams on MFMA, shared by both v-heads: N (K K^T, to LDS) and Aqk
-  // (Q K^T, to the workspace).  Q K^T is formed transposed (A = K rows, B = Q
-  // rows): lane (lg, l16) then holds Aqk[16 mi + l16][16 ni + 4 lg + rr], which
-  // is exactly half (slots 4 (ni & 1) .. +3) of fragment (mi, ni >> 1) in
-  // permuted fragment order.  Wave w forms lower tiles w and w + 8 (< 10). ----
-  uint16_t* frag2[kGva];
-#pragma unroll
-  for (int e = 0; e < kGva; ++e)
-    frag2[e] = ws_frag + (static_cast<size_t>(r) * kVHeads + kGva * hq + e) * kFrags * kMatElems;
-  const int rsw = kq_swz(l16);
-  f32x4 akk[2], aqk[2];
-#pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    int mi, ni;
-    lower_tile(min(w + 8 * n, 9), mi, ni);
-    akk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-    aqk[n] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const int at = 8 * ((4 * d + lg) ^ rsw);
-      const bf16x8 km = *reinterpret_cast<const bf16x8*>(&sm.u.kq[0][16 * mi + l16][at]);
-      const bf16x8 kn = *reinterpret_cast<const bf16x8*>(&sm.u.kq[0][16 * ni + l16][at]);
-      const bf16x8 qm = *reinterpret_cast<const bf16x8*>(&sm.u.kq[1][16 * mi + l16][at]);
-      akk[n] = mfma16(km, kn, akk[n]);
-      aqk[n] = mfma16(kn, qm, aqk[n]);
-    }
-  }
-#pragma unroll
-  for (int n = 0; n < 2; ++n) {
-    if (w + 8 * n >= 10) break;   // wave-uniform
-    int mi, ni;
-    lower_tile(w + 8 * n, mi, ni);
+    // ---- loads: gates (lane = token), K / Q rows as MFMA fragments ----
+    // fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
+    // columns 32 d + 8 lg .. + 7.  Rows past the chunk end repeat row c - 1:
+    // they meet beta = 0 (rows of N), i <= t masks and output rows never stored.
+    const size_t gi = static_cast<size_t>(t0 + min(lane, cm1)) * kVHeads + kGva * hq + e0;
+    float a_t[kGva], b_t[kGva];
 #pragma unroll
     for (int e = 0; e < kGva; ++e) {
-      {
-        // akk[n][rr] = K_t . K_i, t = 16 mi + 4 lg + rr, i = 16 ni + l16
-        const int i = 16 * ni + l16;
-        const float gi_ = sm.lgam[e][i];
-        const f32x4 gt = *reinterpret_cast<const f32x4*>(&sm.lgam[e][16 * mi + 4 * lg]);
-        const f32x4 bt = *reinterpret_cast<const f32x4*>(&sm.beta[e][16 * mi + 4 * lg]);
+      a_t[e] = e < ne ? bf2f(a[gi + e]) : 0.0f;
+      b_t[e] = e < ne ? bf2f(b[gi + e]) : 0.0f;
+    }
+    bf16x8 kf[4][4], qf[4][4];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int t = 16 * mi + 4 * lg + rr;
-          sm.nm[e][t][i] = i < t ? bt[rr] * fast_exp2(gt[rr] - gi_) * akk[n][rr] : 0.0f;
-        }
-        if (mi == ni) {   // diagonal tile: |k_t|^2 (rows t >= c have beta = 0 and contribute 0)
+    for (int m = 0; m < 4; ++m) {
+      const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
+      const uint16_t* kr = k + (row * kQKHeads + hq) * kDim + 8 * lg;
+      const uint16_t* qr = q + (row * kQKHeads + hq) * kDim + 8 * lg;
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-            if (l16 == 4 * lg + rr)
-              sm.kb2[e][i] = __log2f(fmaxf(1.0f, fabsf(1.0f - bt[rr] * akk[n][rr])));
-        }
-      }
-      {
-        // aqk[n][rr] = K_i . Q_t (transposed), i = 16 ni + 4 lg + rr, t = 16 mi + l16
-        const int t = 16 * mi + l16;
-        const float gt = sm.lgam[e][t];
-        const f32x4 gi4 = *reinterpret_cast<const f32x4*>(&sm.lgam[e][16 * ni + 4 * lg]);
-        float x[4];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int i = 16 * ni + 4 * lg + rr;
-          x[rr] = i <= t ? fast_exp2(gt - gi4[rr]) * aqk[n][rr] : 0.0f;
-        }
-        *reinterpret_cast<u32x2*>(frag2[e] + kMatElems + (frag_slot(mi, ni >> 1) * 64 + lane) * 8 + 4 * (ni & 1)) =
-            u32x2{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3])};
+      for (int d = 0; d < 4; ++d) {
+        kf[m][d] = *reinterpret_cast<const bf16x8*>(kr + 32 * d);
+        qf[m][d] = *reinterpret_cast<const bf16x8*>(qr + 32 * d);
       }
     }
-  }
-  // the stored half-fragments of Aqk above the diagonal, both v-heads: tiles
-  // (mi, ni) = (0, 1) in fragment (0, 0) and (2, 3) in fragment (2, 1)
-  if (tid < kGva * 2 * 64) {
-    const int e = tid >> 7, zl = tid & 63;
-    const int mi = (tid & 64) ? 2 : 0, ni = mi + 1;
-    *reinterpret_cast<u32x2*>(frag2[e] + kMatElems + (frag_slot(mi, ni >> 1) * 64 + zl) * 8 + 4 * (ni & 1)) =
-        u32x2{0u, 0u};
-  }
-  __syncthreads();   // N complete; K / Q space becomes T
 
-  // ---- T = (I + N)^{-1} per v-head: diagonal 16x16 blocks by forward substitution ----
-  float (*nmh)[kMRow] = sm.nm[hh];
-  float (*tmh)[kMRow] = sm.u.tm[hh];
-  if (lane < 16) {
-    const int base = 16 * wl;
-    const int j = lane;
-    // column j of T_ii, updated column-wise: once x[i] is final, every later
-    // row subtracts N[r][i] x[i] (the same terms in the same order as the
-    // row-wise recurrence, but with a dependency depth of 16 instead of 120)
-    float x[16];
+    // ---- raw grams, shared by the v-heads of the pair: kk = K K^T (lower
+    // tiles), qk = K Q^T (upper tiles, i.e. Q K^T transposed) ----
+    f32x4 kk[4][4], qk[4][4];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = (i == j) ? 1.0f : 0.0f;
+    for (int m = 0; m < 4; ++m) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i)
+      for (int n = 0; n <= m; ++n) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = i + 1; r < 16; ++r) x[r] = fmaf(-nmh[base + r][base + i], x[i], x[r]);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) tmh[base + i][base + j] = x[i];
-  }
-
-  // ---- off-diagonal blocks by distance on fp32 MFMA:
-  //      T_ij = -T_ii P,  P = sum_{m=j}^{i-1} N_im T_mj
-#pragma unroll
-  for (int dist = 1; dist < 4; ++dist) {
-    __syncthreads();
-    if (wl < 4 - dist) {
-      const int bj = wl, bi = wl + dist;
-      // one accumulator per block product (independent MFMA chains), summed after
-      f32x4 pu[3];
-#pragma unroll
-      for (int u = 0; u < dist; ++u)
-        pu[u] = block_prod(f32x4{0.f, 0.f, 0.f, 0.f}, &nmh[16 * bi][16 * (bj + u)], &tmh[16 * (bj + u)][16 * bj],
-                           l16, lg);
-      f32x4 pacc = pu[0];
-#pragma unroll
-      for (int u = 1; u < dist; ++u) pacc += pu[u];
-      // T_ii P with P straight from its C registers: MFMA kc of the product
-      // pairs depth 4 lg + kc, which lane (lg, l16) holds as pacc[kc] =
-      // P[4 lg + kc][l16]; the A operand reads T_ii at the same depth
-      f32x4 tv = {0.f, 0.f, 0.f, 0.f};
-      const float* tii = &tmh[16 * bi][16 * bi];
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) tv = mfma_f32(tii[l16 * kMRow + 4 * lg + kc], pacc[kc], tv);
-      block_store(&tmh[16 * bi][16 * bj], tv, -1.0f, l16, lg);
+        for (int dd = 0; dd < 4; ++dd) {
+          acc = mfma16(kf[m][dd], kf[n][dd], acc);
+          acq = mfma16(kf[n][dd], qf[m][dd], acq);
+        }
+        kk[m][n] = acc;
+        qk[n][m] = acq;
+      }
     }
-  }
-  __syncthreads();
 
-  // ---- pack Tb = T diag(beta) as fp16 (permuted fragment order), per v-head ----
-  // fragment (m, d) at slot f, lane l: row t = 16 m + l % 16, slots s: i = perm_depth(d, l / 16, s)
-  for (int qi = tid & 255; qi < kMatFrags * 64; qi += 256) {
-    const int f = qi >> 6, l = qi & 63;
-    const int m = f < 2 ? f : 2 + ((f - 2) >> 1), d = f < 2 ? 0 : (f & 1);
-    const int t = 16 * m + (l & 15);
-    const int i0 = 32 * d + 4 * (l >> 4);
-    const int e = tid >> 8;
-    const f32x4 ta = *reinterpret_cast<const f32x4*>(&sm.u.tm[e][t][i0]);
-    const f32x4 tb = *reinterpret_cast<const f32x4*>(&sm.u.tm[e][t][i0 + 16]);
-    const f32x4 ba = *reinterpret_cast<const f32x4*>(&sm.beta[e][i0]);
-    const f32x4 bb = *reinterpret_cast<const f32x4*>(&sm.beta[e][i0 + 16]);
-    float x[8];
+    const int h0 = kGva * hq + e0;
+    float alog[kGva], dtb[kGva];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      x[s] = i0 + s <= t ? ta[s] * ba[s] : 0.0f;
-      x[4 + s] = i0 + 16 + s <= t ? tb[s] * bb[s] : 0.0f;
+    for (int e = 0; e < kGva; ++e) {
+      alog[e] = A_log[min(h0 + e, kVHeads - 1)];
+      dtb[e] = dt_bias[min(h0 + e, kVHeads - 1)];
     }
-    *reinterpret_cast<u32x4*>(frag2[e] + qi * 8) =
-        u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
-  }
-
-  // the chunk's map bound: sum over tokens of log2 g_t + log2 max(1, |1 - beta_t |k_t|^2|)
-  if (wl == 0) {
-    const float lb = wave_sumf(sm.kb2[hh][lane]) + sm.lgam[hh][c - 1];
-    if (lane == 0) ws_gam[(static_cast<size_t>(r) * kVHeads + h) * kGamStride + kBoundAt] = lb;
-  }
+    uint16_t* frag0 = ws_frag + (static_cast<size_t>(r) * kVHeads + h0) * kFrags * kMatElems;
+    float* gp0 = ws_gam + (static_cast<size_t>(r) * kVHeads + h0) * kGamStride;
+    if (pair_items)
+      prepass_heads<kGva>(ws, kk, qk, c, a_t, b_t, alog, dtb, frag0, gp0);
+    else
+      prepass_heads<1>(ws, kk, qk, c, a_t, b_t, alog, dtb, frag0, gp0);
   }
 }
 
@@ -2256,7 +2350,10 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (!fused_plan)
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                         total_tokens, Ri, gc, rec_start, recs, lists);
-  const long long g_pre = std::min<long long>(R * kQKHeads, kPrepassMaxGrid - fused_plan);
+  // one wave per (record, v-head), or per (record, q/k head) when those would
+  // not all be resident at once; at most two work-groups per CU
+  const long long pre_items = R * kVHeads > kPrepassResident ? R * kQKHeads : R * kVHeads;
+  const long long g_pre = std::min<long long>((pre_items + kPrepassWaves - 1) / kPrepassWaves, kPrepassMaxGroups);
   prepass_kernel<<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
       qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
       Ri, gc, fused_plan, rec_start, lists, frag, gam);
