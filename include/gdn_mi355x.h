@@ -55,11 +55,20 @@ int gdn_decode_fwd(const void* q, const void* k, const void* v, const float* sta
                    float scale, void* out, float* new_state, int batch, int rows_per_wave,
                    void* stream);
 
-/* Workspace size in bytes that gdn_prefill_fwd needs for `num_seqs` sequences
+/* Default workspace size in bytes for gdn_prefill_fwd with `num_seqs` sequences
  * and `total_tokens` tokens (the caller allocates it; its contents on entry are
  * irrelevant).  The reference allocates the same kind of scratch per call with
- * torch.empty (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:132-218). */
+ * torch.empty (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:132-218).
+ * About 3.6 KiB per token plus up to 48 MiB of segment slots (1 MiB each); a
+ * larger workspace gives the planner more slots, a smaller one (down to
+ * gdn_prefill_workspace_min_bytes) fewer.  Results do not depend on it. */
 size_t gdn_prefill_workspace_bytes(int num_seqs, long long total_tokens);
+
+/* Smallest workspace gdn_prefill_fwd accepts: no segment slots, so no sequence
+ * is cut into segments that run concurrently (long sequences run their chunks
+ * one after the other).  No reference counterpart: it states the floor of the
+ * workspace contract above. */
+size_t gdn_prefill_workspace_min_bytes(int num_seqs, long long total_tokens);
 
 /* Prefill: chunked recurrence over a cu_seqlens ragged batch.
  *
@@ -77,7 +86,8 @@ size_t gdn_prefill_workspace_bytes(int num_seqs, long long total_tokens);
  *   scale       0 selects 1/sqrt(128)
  *   output      [total_tokens, 8, 128] bf16 (written, 8-byte aligned; rows outside every sequence untouched)
  *   new_state   [num_seqs, 8, 128, 128] fp32 (written; 16-byte aligned; must not be `state`)
- *   workspace   device scratch of at least gdn_prefill_workspace_bytes() bytes, 256-byte aligned
+ *   workspace   device scratch of at least gdn_prefill_workspace_min_bytes() bytes (normally
+ *               gdn_prefill_workspace_bytes()), 256-byte aligned; workspace_bytes is its size
  */
 int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
                     const float* A_log, const void* a, const float* dt_bias, const void* b,

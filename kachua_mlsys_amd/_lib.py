@@ -42,6 +42,7 @@ SIGNATURES = {
     "gdn_decode_fwd": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_float,
                                       _VP, _VP, ctypes.c_int, ctypes.c_int, _VP]),
     "gdn_prefill_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_longlong]),
+    "gdn_prefill_workspace_min_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_longlong]),
     "gdn_prefill_fwd": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_int,
                                        ctypes.c_int, ctypes.c_longlong, ctypes.c_float, _VP, _VP,
                                        _VP, ctypes.c_size_t, _VP]),

@@ -181,10 +181,13 @@ __host__ __device__ inline long long max_records(int num_seqs, long long tokens)
   return (tokens + kChunk - 1) / kChunk + num_seqs;
 }
 
-__host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
+// Layout for gcap segment slots (0 .. max_segments(tokens)): the planner only
+// picks segment lengths whose slots fit, so any gcap gives the same results;
+// with none, no sequence is segmented and the M-run outputs need no storage.
+__host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens, long long gcap) {
   WsLayout L;
   const size_t R = static_cast<size_t>(max_records(num_seqs, tokens));
-  const size_t G = static_cast<size_t>(max_segments(tokens));
+  const size_t G = static_cast<size_t>(gcap);
   const size_t N = static_cast<size_t>(num_seqs);
   size_t off = 0;
   L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kMatElems * sizeof(uint16_t));
@@ -194,12 +197,29 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens) {
   L.rec_off = off;   off = align256(off + R * sizeof(int4));
   L.slotb_off = off; off = align256(off + G * kVHeads * kHeadState * sizeof(float));
   L.slotm_off = off; off = align256(off + G * kVHeads * kMSlotElems * sizeof(uint16_t));
-  L.oi_off = off;    off = align256(off + static_cast<size_t>(tokens) * kVHeads * kDim * sizeof(uint16_t));
+  L.oi_off = off;    off = align256(off + (G > 0 ? static_cast<size_t>(tokens) : 0) * kVHeads * kDim * sizeof(uint16_t));
   L.mval_off = off;  off = align256(off + G * kVHeads * sizeof(int));
   // a block covers formed chunks of one M-run, whose records are its own: at most 8 R blocks
   L.fix_off = off;   off = align256(off + R * kVHeads * 2 * sizeof(int4));
   L.total = off;
   return L;
+}
+
+// Segment slots of the default workspace: each costs 1 MiB (a state and a
+// segment map per v-head).  The planner's best segmentings of the benchmark
+// batches use at most a few dozen (16 sequences of 16384 tokens: 10).
+constexpr long long kDefaultSlots = 48;
+
+// The most slots (up to what the batch can use) whose layout fits `bytes`, or
+// -1 when not even the layout without slots fits.
+inline long long slots_fitting(int num_seqs, long long tokens, size_t bytes) {
+  long long lo = 0, hi = max_segments(tokens);
+  if (ws_layout(num_seqs, tokens, 0).total > bytes) return -1;
+  while (lo < hi) {   // the layout grows with gcap
+    const long long mid = lo + (hi - lo + 1) / 2;
+    if (ws_layout(num_seqs, tokens, mid).total <= bytes) lo = mid; else hi = mid - 1;
+  }
+  return lo;
 }
 
 // Sequence bounds from cu_seqlens, clamped into [0, T] with end >= start.
@@ -2287,7 +2307,12 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
 
 extern "C" size_t gdn_prefill_workspace_bytes(int num_seqs, long long total_tokens) {
   if (num_seqs < 0 || total_tokens < 0) return 0;
-  return gdn::ws_layout(num_seqs, total_tokens).total;
+  return gdn::ws_layout(num_seqs, total_tokens, std::min(gdn::max_segments(total_tokens), gdn::kDefaultSlots)).total;
+}
+
+extern "C" size_t gdn_prefill_workspace_min_bytes(int num_seqs, long long total_tokens) {
+  if (num_seqs < 0 || total_tokens < 0) return 0;
+  return gdn::ws_layout(num_seqs, total_tokens, 0).total;
 }
 
 extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
@@ -2315,13 +2340,14 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   if (reinterpret_cast<uintptr_t>(workspace) & 255u) return GDN_ERR_UNALIGNED;
   if (state != nullptr && state == new_state) return GDN_ERR_ALIASING;
   const long long R = max_records(num_seqs, total_tokens);
-  const long long gcap = max_segments(total_tokens);
   // every work-item index (records x heads, runs x 16, multi-segment entries x 64) fits an int
   if (R * kVHeads + static_cast<long long>(num_seqs) * kVHeads * 8 > 0x7fffffffLL ||
-      max_runs(num_seqs, gcap) * 2 * kVHeads > 0x7fffffffLL)
+      max_runs(num_seqs, max_segments(total_tokens)) * 2 * kVHeads > 0x7fffffffLL)
     return GDN_ERR_INVALID_ARGUMENT;
-  const WsLayout L = ws_layout(num_seqs, total_tokens);
-  if (workspace_bytes < L.total) return GDN_ERR_WORKSPACE_TOO_SMALL;
+  // as many segment slots as the workspace holds (the planner adapts to them)
+  const long long gcap = slots_fitting(num_seqs, total_tokens, workspace_bytes);
+  if (gcap < 0) return GDN_ERR_WORKSPACE_TOO_SMALL;
+  const WsLayout L = ws_layout(num_seqs, total_tokens, gcap);
   if (!(scale > 0.0f) && !(scale < 0.0f)) scale = 0.08838834764831845f;
 
   char* ws = static_cast<char*>(workspace);
@@ -2365,8 +2391,8 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   consumer_kernel<<<dim3(static_cast<unsigned>(g_long + g_short)), dim3(kSplitThreads), 0, st>>>(
       qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, Ri, gc, scale, rec_start, lists,
       num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm, mval, fix);
-  // a second segment needs more than kMinSegChunks chunks in one sequence
-  if (total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
+  // a second segment needs more than kMinSegChunks chunks in one sequence and a slot
+  if (gcap > 0 && total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
     const long long g_fin = std::min<long long>(R * kVHeads, 1024);
     finish_kernel<<<dim3(static_cast<unsigned>(g_fin)), dim3(kFinThreads), 0, st>>>(
         lists, num_seqs, gc, fix, static_cast<int>(R * kVHeads), slotb, slotm, mval, oi, ob, new_state);

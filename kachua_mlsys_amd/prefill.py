@@ -22,7 +22,14 @@ HEAD_DIM = 128
 
 
 def workspace_bytes(num_seqs: int, total_tokens: int) -> int:
+    """Default workspace size (what launch_gdn allocates when none is given)."""
     return int(_lib.load().gdn_prefill_workspace_bytes(int(num_seqs), int(total_tokens)))
+
+
+def workspace_min_bytes(num_seqs: int, total_tokens: int) -> int:
+    """Smallest accepted workspace: no segment slots (long sequences then run
+    their chunks one after the other); results are the same."""
+    return int(_lib.load().gdn_prefill_workspace_min_bytes(int(num_seqs), int(total_tokens)))
 
 
 def launch_gdn(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, output=None,
@@ -32,7 +39,8 @@ def launch_gdn(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, out
     q, k [T,4,128] bf16; v [T,8,128] bf16; state [N,8,128,128] fp32 or None;
     A_log, dt_bias [8] fp32; a, b [T,8] bf16; cu_seqlens [N+1] int32/int64.
     ``workspace`` (optional) is a uint8 GPU tensor of at least
-    ``workspace_bytes(N, T)`` bytes; by default one is taken from torch's
+    ``workspace_min_bytes(N, T)`` bytes (``workspace_bytes(N, T)`` gives the
+    default number of segment slots); by default one is taken from torch's
     caching allocator per call, as the reference does with torch.empty.
     """
     q, k, v = as_tensor(q, "q"), as_tensor(k, "k"), as_tensor(v, "v")
@@ -76,11 +84,11 @@ def launch_gdn(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, out
     if N == 0:
         return output, new_state
     lib = _lib.load()
-    need = int(lib.gdn_prefill_workspace_bytes(N, T))
     if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        workspace = torch.empty(int(lib.gdn_prefill_workspace_bytes(N, T)), dtype=torch.uint8, device=dev)
     else:
         check_device(workspace, "workspace")
+        need = int(lib.gdn_prefill_workspace_min_bytes(N, T))
         if workspace.dtype != torch.uint8 or not workspace.is_contiguous() or workspace.numel() < need:
             raise ValueError(f"workspace: need a contiguous uint8 tensor of >= {need} bytes")
     with torch.cuda.device(dev):

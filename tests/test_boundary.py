@@ -50,6 +50,19 @@ def test_workspace_bytes_monotone(lib):
     assert all(x % 256 == 0 for x in w)
     assert w[0] < w[1] < w[2] < w[3]
     assert lib.gdn_prefill_workspace_bytes(-1, 10) == 0
+    assert lib.gdn_prefill_workspace_min_bytes(-1, 10) == 0
+    for n, t in ((1, 64), (2, 65), (16, 16384), (1, 1 << 20)):
+        assert lib.gdn_prefill_workspace_min_bytes(n, t) <= lib.gdn_prefill_workspace_bytes(n, t)
+
+
+def test_workspace_size_c3_and_growth(lib):
+    # configuration 3 (16 sequences, 16384 tokens): the default workspace stays
+    # below the call's own algorithmic traffic (117,964,864 bytes)
+    assert lib.gdn_prefill_workspace_bytes(16, 16384) <= 117_964_864
+    # about 3.6 KiB per token beyond the default slots, not the ~10 KiB per
+    # token of slots sized for the shortest segments
+    big = lib.gdn_prefill_workspace_bytes(1, 1 << 20)
+    assert big <= (1 << 20) * 3800 + (64 << 20), big
 
 
 NULL = None
@@ -77,12 +90,13 @@ def test_c_prefill_rejects_before_launch(lib):
     f = lib.gdn_prefill_fwd
     ins = [A16] * 8
     need = lib.gdn_prefill_workspace_bytes(2, 100)
+    floor = lib.gdn_prefill_workspace_min_bytes(2, 100)
     base = ins + [A16, 0, 2, 100, 0.0, A16, A16b, A16, need, NULL]
     x = list(base); x[11] = -1                                              # negative T
     assert f(*x) == -1
     x = list(base); x[15] = NULL                                            # no workspace
     assert f(*x) == -1
-    x = list(base); x[16] = need - 1                                        # workspace too small
+    x = list(base); x[16] = floor - 1                                       # workspace too small
     assert f(*x) == -2
     x = list(base); x[15] = A16 + 16                                        # workspace not 256B aligned
     assert f(*x) == -3

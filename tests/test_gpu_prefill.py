@@ -218,3 +218,18 @@ def test_prefill_exhausted_records_is_safe(gpu):
     assert state_rel(ns[0], s_ref[0]) <= 2e-3
     assert torch.isfinite(ns).all()
     assert not ns[1].any()   # the decreasing pair is an empty sequence
+
+
+@pytest.mark.parametrize("slots", [0, 2, None])
+def test_prefill_workspace_slots(gpu, slots):
+    # the planner uses as many segment slots as the workspace holds: none (the
+    # smallest accepted workspace: every sequence runs unsegmented), two, or the
+    # default number; results stay within tolerance either way
+    p = prefill_inputs_from_lengths([3000, 1500, 700, 40], seed=33)
+    T, N = p.q.shape[0], len(p.lengths)
+    if slots is None:
+        nbytes = prefill.workspace_bytes(N, T)
+    else:
+        nbytes = prefill.workspace_min_bytes(N, T) + slots * (1 << 20)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
+    _check(p, gpu, f"prefill workspace with {slots} extra slots", workspace=ws)
