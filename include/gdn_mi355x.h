@@ -19,15 +19,19 @@
 extern "C" {
 #endif
 
-#define GDN_ABI_VERSION 1
+#define GDN_ABI_VERSION 2
 
 enum {
   GDN_OK = 0,
   GDN_ERR_INVALID_ARGUMENT = -1,   /* null pointer, negative size, bad option */
   GDN_ERR_WORKSPACE_TOO_SMALL = -2,
   GDN_ERR_UNALIGNED = -3,          /* a buffer misses its required alignment */
-  GDN_ERR_ALIASING = -4            /* state and new_state are the same buffer */
+  GDN_ERR_ALIASING = -4,           /* state and new_state are the same buffer */
+  GDN_ERR_TOO_LARGE = -5           /* batch needs more than the no-allocation scratch */
 };
+
+/* Size of the device scratch array behind gdn_prefill_fwd_noalloc (per GPU). */
+#define GDN_PREFILL_NOALLOC_SCRATCH_BYTES (128u << 20)
 
 /* ABI version of the loaded library (GDN_ABI_VERSION it was built with). */
 int gdn_abi_version(void);
@@ -94,6 +98,25 @@ int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* st
                     const void* cu_seqlens, int cu_seqlens_is_int64, int num_seqs,
                     long long total_tokens, float scale, void* output, float* new_state,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Prefill that allocates nothing: gdn_prefill_fwd with its workspace taken from
+ * a file-scope device array of GDN_PREFILL_NOALLOC_SCRATCH_BYTES (128 MiB),
+ * which each GPU the library runs on holds until the process ends.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Arguments as gdn_prefill_fwd without the workspace;
+ * `stream` must belong to the current device.  Returns GDN_ERR_TOO_LARGE when
+ * gdn_prefill_workspace_min_bytes(num_seqs, total_tokens) exceeds the array
+ * (about 30k tokens); up to the default workspace size results equal
+ * gdn_prefill_fwd's with a default workspace.  Every call on one GPU shares that
+ * GPU's array: calls that overlap in time on one GPU (other streams, other host
+ * threads) race and must be ordered by the caller.  Nothing in the array needs
+ * to be cleared between calls. */
+int gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v, const float* state,
+                            const float* A_log, const void* a, const float* dt_bias, const void* b,
+                            const void* cu_seqlens, int cu_seqlens_is_int64, int num_seqs,
+                            long long total_tokens, float scale, void* output, float* new_state,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -46,8 +46,11 @@ SIGNATURES = {
     "gdn_prefill_fwd": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_int,
                                        ctypes.c_int, ctypes.c_longlong, ctypes.c_float, _VP, _VP,
                                        _VP, ctypes.c_size_t, _VP]),
+    "gdn_prefill_fwd_noalloc": (ctypes.c_int, [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, ctypes.c_int,
+                                               ctypes.c_int, ctypes.c_longlong, ctypes.c_float, _VP, _VP,
+                                               _VP]),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def hipcc_path() -> str:

@@ -10,6 +10,7 @@ extern "C" const char* gdn_status_string(int status) {
     case GDN_ERR_WORKSPACE_TOO_SMALL: return "workspace smaller than gdn_prefill_workspace_bytes()";
     case GDN_ERR_UNALIGNED: return "buffer misses its required alignment";
     case GDN_ERR_ALIASING: return "state and new_state must be different buffers";
+    case GDN_ERR_TOO_LARGE: return "batch needs more workspace than the no-allocation scratch holds";
     default: return status > 0 ? "HIP launch error" : "unknown status";
   }
 }

@@ -42,6 +42,8 @@
 // bf16.  The fp32 state never leaves registers between chunks.
 #include "gdn_common.h"
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 #include "../../include/gdn_mi355x.h"
 
@@ -2315,13 +2317,15 @@ extern "C" size_t gdn_prefill_workspace_min_bytes(int num_seqs, long long total_
   return gdn::ws_layout(num_seqs, total_tokens, 0).total;
 }
 
-extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
-                               const float* A_log, const void* a, const float* dt_bias,
-                               const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
-                               int num_seqs, long long total_tokens, float scale, void* output,
-                               float* new_state, void* workspace, size_t workspace_bytes,
-                               void* stream) {
-  using namespace gdn;
+namespace gdn {
+
+// The prefill launches for a workspace of workspace_bytes bytes (both entry
+// points below): argument checks first, nothing launched on a rejection.
+static int prefill_launch(const void* q, const void* k, const void* v, const float* state,
+                          const float* A_log, const void* a, const float* dt_bias,
+                          const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
+                          int num_seqs, long long total_tokens, float scale, void* output,
+                          float* new_state, void* workspace, size_t workspace_bytes, void* stream) {
   if (num_seqs < 0 || total_tokens < 0) return GDN_ERR_INVALID_ARGUMENT;
   if (num_seqs == 0) return GDN_OK;
   if (!cu_seqlens || !new_state || !workspace || !A_log || !dt_bias)
@@ -2399,4 +2403,72 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
+}
+
+// ---- no-allocation variant: the workspace is a file-scope device array ----
+// Each GPU the library runs on holds one copy until the process ends.  Host
+// code never passes the array's name to a kernel (on the host it is only a
+// stand-in for the symbol): the device address comes from hipGetSymbolAddress,
+// taken once per device with that device current, on the entry point's first
+// call there.
+static_assert(GDN_PREFILL_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
+static __device__ __align__(256) unsigned char scratch[GDN_PREFILL_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array (its first call on a
+// device resolves the symbol).  Returns GDN_OK or an error code.
+static int current_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return GDN_ERR_INVALID_ARGUMENT;
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (p == nullptr) return GDN_ERR_INVALID_ARGUMENT;
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return GDN_OK;
+}
+
+}  // namespace gdn
+
+extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
+                               const float* A_log, const void* a, const float* dt_bias,
+                               const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
+                               int num_seqs, long long total_tokens, float scale, void* output,
+                               float* new_state, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64, num_seqs,
+                             total_tokens, scale, output, new_state, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v, const float* state,
+                                       const float* A_log, const void* a, const float* dt_bias,
+                                       const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
+                                       int num_seqs, long long total_tokens, float scale, void* output,
+                                       float* new_state, void* stream) {
+  using namespace gdn;
+  if (num_seqs < 0 || total_tokens < 0) return GDN_ERR_INVALID_ARGUMENT;
+  if (num_seqs == 0) return GDN_OK;
+  if (gdn_prefill_workspace_min_bytes(num_seqs, total_tokens) > GDN_PREFILL_NOALLOC_SCRATCH_BYTES)
+    return GDN_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  const int st = current_scratch(&ws);
+  if (st != GDN_OK) return st;
+  // the default workspace's slot count when it fits, so results equal
+  // gdn_prefill_fwd's with a default workspace
+  const size_t bytes = std::min<size_t>(GDN_PREFILL_NOALLOC_SCRATCH_BYTES,
+                                        gdn_prefill_workspace_bytes(num_seqs, total_tokens));
+  return prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64, num_seqs,
+                        total_tokens, scale, output, new_state, ws, bytes, stream);
 }

@@ -39,9 +39,9 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_status_text(lib):
-    assert lib.gdn_abi_version() == 1
+    assert lib.gdn_abi_version() == 2
     assert lib.gdn_status_string(0) == b"ok"
-    for code in (-1, -2, -3, -4):
+    for code in (-1, -2, -3, -4, -5):
         assert b"unknown" not in lib.gdn_status_string(code)
 
 
@@ -177,3 +177,18 @@ def test_solution_dirs_point_at_entry_points(definition, module):
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
     assert getattr(mod, fn) is module.launch_gdn
+
+
+def test_c_prefill_noalloc_rejects_before_launch(lib):
+    # the no-allocation entry point: rejected sizes and arguments launch nothing
+    f = lib.gdn_prefill_fwd_noalloc
+    ins = [A16] * 8
+    base = ins + [A16, 0, 2, 100, 0.0, A16, A16b, NULL]
+    x = list(base); x[11] = -1                                              # negative T
+    assert f(*x) == -1
+    x = list(base); x[10] = 0                                               # no sequences: no-op
+    assert f(*x) == 0
+    big = 1 << 20                                                           # beyond the scratch array
+    assert lib.gdn_prefill_workspace_min_bytes(2, big) > (128 << 20)
+    x = list(base); x[11] = big
+    assert f(*x) == -5
