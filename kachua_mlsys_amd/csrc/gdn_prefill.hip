@@ -62,6 +62,9 @@ constexpr int kBoundAt = 2 * kChunk;
 // and all later outputs are below 2^-60 of the state they multiply and the run
 // stops.
 constexpr float kNegligibleLog2 = -60.0f;
+// Chunks whose map bound is above this (log2) carry the state into X = K S^T
+// as a bf16 hi + lo pair instead of one bf16 (see chain_chunk).
+constexpr float kHiLoBoundLog2 = -8.0f;
 constexpr int kMNegligible = 1 << 30;   // flag in the M-run table: the run stopped early, its map is negligible
 constexpr int kFrags = 2;                    // per (record, v-head): Tb (fp16), Aqk (bf16)
 
@@ -1177,6 +1180,27 @@ __device__ __forceinline__ f16x8 half_frag(const float (&x)[8]) {
                                          pack_h2(x[4], x[5]), pack_h2(x[6], x[7])});
 }
 
+// Power-of-two scale for the fp16 conversion of R = V - gam X (one value per
+// wave): 1 while every |R| of the wave is below 2^15 and at least one reaches
+// 2^-4 (checked with two ballots, no cross-lane reduction); otherwise the wave
+// maximum goes to [2^10, 2^11), so R keeps fp16's 11 significant bits at any
+// magnitude.  Zero, inf and NaN maxima keep scale 1 (they pass through as in
+// fp32).  The caller divides Delta = Tb R by the same power of two.
+__device__ __forceinline__ float r_scale(const f32x4 (&Rt)[4]) {
+  float mx = 0.0f;
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) mx = fmaxf(mx, fabsf(Rt[m][rr]));
+  const bool big = __builtin_amdgcn_ballot_w64(mx >= 32768.0f) != 0;
+  const bool small = __builtin_amdgcn_ballot_w64(mx >= 0.0625f) == 0;
+  if (!big && !small) return 1.0f;
+  const int bits = wave_max0(__float_as_int(mx));   // non-negative floats order as integers
+  if (bits == 0 || bits >= 0x7f800000) return 1.0f;
+  const int e = max((bits >> 23) - 127, -117);      // floor(log2 max), subnormals clamped
+  return __int_as_float((137 - e) << 23);           // 2^(10 - e)
+}
+
 __device__ __forceinline__ bf16x8 round_frag(const float (&x)[8]) {
   return __builtin_bit_cast(bf16x8, u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]),
                                           pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])});
@@ -1296,6 +1320,11 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[m][rr] * X[m][rr];
   }
+  const float rsc = r_scale(Rt);
+  if (rsc != 1.0f) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Rt[m] = Rt[m] * rsc;
+  }
   f16x8 rf[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
@@ -1311,6 +1340,11 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
     for (int d = 0; d < 2; ++d)
       if (!frag_zero(m, d))
         D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][(frag_slot(m, d) * 64 + lane) * 8]), rf[d], D[m]);
+  }
+  if (rsc != 1.0f) {
+    const float inv = 1.0f / rsc;   // exact: a power of two
+#pragma unroll
+    for (int m = 0; m < 4; ++m) D[m] = D[m] * inv;
   }
 
   // ---- Delta as bf16 (output) and Delta' = tail Delta as hi + lo (state) ----
@@ -1615,6 +1649,17 @@ __device__ __forceinline__ void state_frags(const f32x4 (&st)[8], bf16x8 (&sb)[4
   }
 }
 
+// Same fragments as a bf16 hi + lo pair (lo = bf16 of the rounding residue).
+__device__ __forceinline__ void state_frags_hilo(const f32x4 (&st)[8], bf16x8 (&hi)[4], bf16x8 (&lo)[4]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    float x[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) x[s] = st[2 * d + (s >> 2)][s & 3];
+    split_frag(x, hi[d], lo[d]);
+  }
+}
+
 // Chain wave, one chunk: S^T tile st (kappa k order, as in consumer_chunk).
 // Each phase issues all of its LDS operand reads before its first product and
 // runs its products over independent accumulators, so neither the LDS latency
@@ -1640,18 +1685,35 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
     gam[m] = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
     vw[m] = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
   }
+  // ---- X = K S^T.  S enters as one bf16, or as a bf16 hi + lo pair when
+  // the chunk's map bound says the state barely decays: then the rounding of
+  // S here is what accumulates over a long sequence (single bf16: state error
+  // 1.2e-3 to 1.5e-3 at 4k to 28k tokens of near-1 decay; hi + lo: 3e-4 to
+  // 4e-4).  Where the map contracts by 2^-8 or more per chunk, earlier
+  // roundings do not accumulate and one bf16 suffices. ----
   bf16x8 sb[4];
-  state_frags(st, sb);
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- X = K S^T ----
   f32x4 X[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (sm.gt[P][kBoundAt] > kHiLoBoundLog2) {   // uniform
+    bf16x8 sbl[4];
+    state_frags_hilo(st, sb, sbl);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int d = 0; d < 4; ++d)
+    for (int d = 0; d < 4; ++d)
 #pragma unroll
-    for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[d][m], sb[d], X[m]);
+      for (int m = 0; m < 4; ++m) {
+        X[m] = mfma16(ka[d][m], sbl[d], X[m]);
+        X[m] = mfma16(ka[d][m], sb[d], X[m]);
+      }
+  } else {
+    state_frags(st, sb);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[d][m], sb[d], X[m]);
+  }
   // Tb fragments land while X runs
   f16x8 tb[2][4];
 #pragma unroll
@@ -1669,6 +1731,11 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) Rt[m][rr] = vv[rr] - gam[m][rr] * X[m][rr];
   }
+  const float rsc = r_scale(Rt);
+  if (rsc != 1.0f) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) Rt[m] = Rt[m] * rsc;
+  }
   f16x8 rf[2];
 #pragma unroll
   for (int d = 0; d < 2; ++d) {
@@ -1684,6 +1751,11 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
 #pragma unroll
     for (int m = 0; m < 4; ++m)
       if (!frag_zero(m, d)) D[m] = mfma16h(tb[d][m], rf[d], D[m]);
+  if (rsc != 1.0f) {
+    const float inv = 1.0f / rsc;   // exact: a power of two
+#pragma unroll
+    for (int m = 0; m < 4; ++m) D[m] = D[m] * inv;
+  }
 
   // operands of the state update, read while Delta forms: tail gates and the
   // K^T fragments (tile kt, row i of the A operand is k = kappa(kt, i/4, i%4);

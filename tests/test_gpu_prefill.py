@@ -60,7 +60,8 @@ def test_prefill_segmented_weak_decay(gpu, lengths):
     _check(p, gpu, f"prefill segmented weak decay {lengths}")
 
 
-@pytest.mark.parametrize("lengths,weak", [([32768], False), ([16384], True), ([12000, 9000, 50, 7000], True)])
+@pytest.mark.parametrize("lengths,weak", [([32768], False), ([16384], True), ([12000, 9000, 50, 7000], True),
+                                           ([32768], True)])
 def test_prefill_very_long(gpu, lengths, weak):
     # hundreds of chunks in one sequence: the planner's long segment lengths,
     # many segments and, with near-1 decay, a scan across every segment map
@@ -233,3 +234,21 @@ def test_prefill_workspace_slots(gpu, slots):
         nbytes = prefill.workspace_min_bytes(N, T) + slots * (1 << 20)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=gpu)
     _check(p, gpu, f"prefill workspace with {slots} extra slots", workspace=ws)
+
+
+@pytest.mark.parametrize("vs", [1e-6, 1e-4, 1e3, 1e5])
+def test_prefill_value_range(gpu, vs):
+    # R = V - gam K S^T enters an fp16 MFMA operand: a power-of-two scale per
+    # wave keeps it inside fp16's range and precision at any magnitude of v
+    # (and of the state, scaled alike); unscaled, v x 1e-6 loses precision in
+    # fp16 subnormals and v x 1e5 overflows
+    p = prefill_inputs_from_lengths([1024, 300, 40], seed=71)
+    p.v = (p.v.float() * vs).to(torch.bfloat16)
+    p.state = p.state * vs
+    print(f"[case] v scale {vs:g}", flush=True)
+    o_ref, s_ref, o32 = prefill_ref(*p.args(), return_fp32_out=True)
+    out, ns = prefill.launch_gdn(*p.to(gpu).args())
+    torch.cuda.synchronize()
+    # outputs scale with v: compare at the scale of the reference
+    sc = float(o32.abs().max())
+    assert_parity(out.float() / sc, ns, o32 / sc, s_ref, f"prefill v x {vs:g}")
