@@ -72,6 +72,50 @@ def _compile(sources, target: Path, verbose: bool) -> Path:
             raise RuntimeError(f"hipcc failed ({res.returncode}):\n{res.stderr}")
         if verbose:
             print(" ".join(cmd))
+        os.chmod(tmp, 0o755)   # readable by whoever runs it (the GPU box's user)
+        os.replace(tmp, target)
+    finally:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+    return target
+
+
+def binding_path() -> Path:
+    import sysconfig
+
+    return LIB_DIR / ("_gdn_torch" + sysconfig.get_config_var("EXT_SUFFIX"))
+
+
+def build_binding(verbose: bool = False) -> Path:
+    """Compile the torch binding (csrc/gdn_torch_binding.cpp) with the host
+    compiler against torch's headers and LIB_PATH (found next to it at run time)."""
+    import sysconfig
+
+    import torch
+    from torch.utils import cpp_extension
+
+    target = binding_path()
+    fd, tmp = tempfile.mkstemp(prefix="_gdn_torch.", suffix=".so.tmp", dir=LIB_DIR)
+    os.close(fd)
+    cxx = shutil.which("c++") or shutil.which("g++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler for the torch binding")
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC",
+           "-DTORCH_EXTENSION_NAME=_gdn_torch", "-DTORCH_API_INCLUDE_EXTENSION_H",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-isystem{d}" for d in cpp_extension.include_paths()],
+           f"-isystem{sysconfig.get_paths()['include']}", f"-I{INCLUDE_DIR}",
+           str(CSRC_DIR / "gdn_torch_binding.cpp"), "-o", tmp,
+           *[f"-L{d}" for d in cpp_extension.library_paths()],
+           "-lc10", "-ltorch_cpu", "-ltorch", "-ltorch_python",
+           f"-L{LIB_DIR}", "-l:" + LIB_PATH.name, "-Wl,-rpath,$ORIGIN"]
+    try:
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"torch binding build failed ({res.returncode}):\n{res.stderr}")
+        if verbose:
+            print(" ".join(cmd))
+        os.chmod(tmp, 0o755)   # readable by whoever runs it (the GPU box's user)
         os.replace(tmp, target)
     finally:
         if os.path.exists(tmp):
@@ -80,10 +124,12 @@ def _compile(sources, target: Path, verbose: bool) -> Path:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile the HIP sources into LIB_PATH and the bandwidth probe into
-    PROBE_PATH (atomic replace of each)."""
+    """Compile the HIP sources into LIB_PATH, the bandwidth probe into
+    PROBE_PATH and the torch binding next to them (atomic replace of each)."""
     _compile(PROBE_SOURCES, PROBE_PATH, verbose)
-    return _compile(SOURCES, LIB_PATH, verbose)
+    path = _compile(SOURCES, LIB_PATH, verbose)
+    build_binding(verbose)
+    return path
 
 
 _LIB = None
@@ -109,6 +155,29 @@ def load() -> ctypes.CDLL:
         raise RuntimeError(f"{LIB_PATH} has ABI version {ver}, expected {ABI_VERSION}; rebuild it")
     _LIB = lib
     return lib
+
+
+_BINDING = None
+
+
+def load_binding():
+    """The torch binding module (built by build()); None when it is not built,
+    in which case the Python entry points validate and call the C ABI through
+    ctypes themselves."""
+    global _BINDING
+    if _BINDING is None:
+        path = binding_path()
+        if not path.exists():
+            _BINDING = False
+        else:
+            import importlib.util
+
+            load()   # the C library first: the binding resolves its symbols there
+            spec = importlib.util.spec_from_file_location("_gdn_torch", path)
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            _BINDING = mod
+    return _BINDING or None
 
 
 _PROBE = None

@@ -29,6 +29,22 @@ def launch_gdn(q, k, v, state, A_log, a, dt_bias, b, scale=None, out=None, new_s
     [B,1,8,128]) bf16 and new_state [B,8,128,128] fp32; returns (out, new_state).
     ``state`` is only read; in-place update (new_state is state) is rejected.
     """
+    # common case first: tensors only, on the current GPU, outputs given ->
+    # checks and launch in the C++ binding (no launch when anything differs;
+    # then the checks below raise the descriptive error)
+    if out is not None and new_state is not None and (scale is None or type(scale) in (float, int)):
+        fast = _lib.load_binding()
+        if fast is not None and type(q) is torch.Tensor:
+            di = q.get_device()
+            if di >= 0 and di == torch._C._cuda_getDevice():
+                try:
+                    st = fast.decode(q, k, v, state, A_log, a, dt_bias, b, 0.0 if scale is None else float(scale),
+                                     out, new_state, rows_per_wave, torch._C._cuda_getCurrentRawStream(di), di)
+                except TypeError:   # an argument that is not a tensor (DLPack producers)
+                    st = fast.NOT_FAST
+                if st != fast.NOT_FAST:
+                    _lib.check(st, "gdn_decode_fwd")
+                    return out, new_state
     q, k, v, state = (as_tensor(x, n) for x, n in ((q, "q"), (k, "k"), (v, "v"), (state, "state")))
     A_log, a, dt_bias, b = (as_tensor(x, n) for x, n in
                             ((A_log, "A_log"), (a, "a"), (dt_bias, "dt_bias"), (b, "b")))

@@ -43,6 +43,23 @@ def launch_gdn(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale=None, out
     default number of segment slots); by default one is taken from torch's
     caching allocator per call, as the reference does with torch.empty.
     """
+    # common case first: tensors only, on the current GPU, outputs given ->
+    # checks and launch in the C++ binding (no launch when anything differs;
+    # then the checks below raise the descriptive error)
+    if output is not None and new_state is not None and (scale is None or type(scale) in (float, int)):
+        fast = _lib.load_binding()
+        if fast is not None and type(q) is torch.Tensor:
+            di = q.get_device()
+            if di >= 0 and di == torch._C._cuda_getDevice():
+                try:
+                    st = fast.prefill(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+                                      0.0 if scale is None else float(scale), output, new_state, workspace,
+                                      torch._C._cuda_getCurrentRawStream(di), di)
+                except TypeError:   # an argument that is not a tensor (DLPack producers)
+                    st = fast.NOT_FAST
+                if st != fast.NOT_FAST:
+                    _lib.check(st, "gdn_prefill_fwd")
+                    return output, new_state
     q, k, v = as_tensor(q, "q"), as_tensor(k, "k"), as_tensor(v, "v")
     state = as_tensor(state, "state")
     A_log, a, dt_bias, b = (as_tensor(x, n) for x, n in

@@ -117,3 +117,21 @@ def test_decode_chain_matches_oracle_chain(gpu):
         o, st = decode.launch_gdn(g.q, g.k, g.v, st, d.A_log.to(gpu), g.a, d.dt_bias.to(gpu), g.b, None)
     torch.cuda.synchronize()
     assert_parity(o, st, o_ref, st_ref, "decode 4-step chain")
+
+
+def test_decode_torch_binding_path(gpu):
+    # outputs given: the C++ binding checks and launches; without them the
+    # Python checks run and ctypes launches.  Both give the same bytes.
+    from kachua_mlsys_amd import _lib
+    assert _lib.load_binding() is not None, "torch binding not built"
+    d = decode_inputs(5, seed=17).to(gpu)
+    o_slow, s_slow = decode.launch_gdn(*d.args())
+    out = torch.empty((5, 8, 128), dtype=torch.bfloat16, device=gpu)
+    ns = torch.empty_like(d.state)
+    o_fast, s_fast = decode.launch_gdn(*d.args(), out, ns)
+    torch.cuda.synchronize()
+    assert o_fast is out and s_fast is ns
+    assert torch.equal(o_fast.view(torch.int16), o_slow.view(torch.int16)) and torch.equal(s_fast, s_slow)
+    # an argument outside the common case still gets the descriptive error
+    with pytest.raises(TypeError, match="q: expected dtype"):
+        decode.launch_gdn(d.q.float(), *d.args()[1:], out, ns)

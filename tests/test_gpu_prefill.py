@@ -252,3 +252,26 @@ def test_prefill_value_range(gpu, vs):
     # outputs scale with v: compare at the scale of the reference
     sc = float(o32.abs().max())
     assert_parity(out.float() / sc, ns, o32 / sc, s_ref, f"prefill v x {vs:g}")
+
+
+def test_prefill_torch_binding_path(gpu):
+    # outputs given: the C++ binding checks and launches; without them the
+    # Python checks run and ctypes launches.  Both give the same bytes.
+    from kachua_mlsys_amd import _lib
+    assert _lib.load_binding() is not None, "torch binding not built"
+    p = prefill_inputs_from_lengths([200, 0, 90], seed=19)
+    g = p.to(gpu)
+    o_slow, s_slow = prefill.launch_gdn(*g.args())
+    out = torch.empty_like(o_slow)
+    ns = torch.empty_like(s_slow)
+    o_fast, s_fast = prefill.launch_gdn(*g.args(), out, ns)
+    torch.cuda.synchronize()
+    assert o_fast is out and s_fast is ns
+    assert torch.equal(o_fast.view(torch.int16), o_slow.view(torch.int16)) and torch.equal(s_fast, s_slow)
+    g.state = None
+    o2, s2 = prefill.launch_gdn(*g.args(), torch.empty_like(out), torch.empty_like(ns))
+    o3, s3 = prefill.launch_gdn(*g.args())
+    torch.cuda.synchronize()
+    assert torch.equal(o2.view(torch.int16), o3.view(torch.int16)) and torch.equal(s2, s3)
+    with pytest.raises(ValueError, match="alias"):
+        prefill.launch_gdn(*p.to(gpu).args()[:3], ns, *g.args()[4:], out, ns)
