@@ -726,11 +726,11 @@ __device__ __forceinline__ void lds_barrier() {
 // rows come straight from global memory into MFMA operand registers (16 bytes
 // of a row per lane is both the A and the B fragment of a gram), the gates sit
 // on the lanes (lane = token), and only the 16x16 diagonal blocks of the
-// triangular inverse pass through LDS.  Two waves per SIMD are resident
-// (kPrepassResident in all).  An item is one (record, v-head) when the batch
-// has at most that many, else one (record, q/k head) whose wave forms the
-// grams once and then runs both v-heads of the GVA pair, so every item of a
-// batch of up to 512 records starts at once.
+// triangular inverse pass through LDS.  An item is one (record, v-head) when
+// the batch has at most 2048 of them (each v-head's phases on its own wave:
+// the shortest latency for a lone item), else one (record, q/k head) whose
+// wave loads the rows and forms the grams once and runs both v-heads of the
+// GVA pair (two waves per SIMD: up to 512 records at once).
 //
 // The inverse is formed transposed: with U = I + N^T (unit upper) and
 // W = U^{-1} = T^T, the 16x16 blocks satisfy
@@ -741,25 +741,37 @@ __device__ __forceinline__ void lds_barrier() {
 constexpr int kPrepassThreads = 256;              // four independent waves
 constexpr int kPrepassWaves = kPrepassThreads / 64;
 constexpr int kPrepassMaxGroups = 512;             // two per CU: eight waves, two per SIMD
-constexpr int kPrepassResident = kPrepassMaxGroups * kPrepassWaves;
 
 struct __align__(16) PrepassWaveSmem {   // per v-head of the item
   float lgam[kGva][kChunk];    // Gam_t / ln 2 (inclusive scan of log2 g)
   float beta[kGva][kChunk];
-  float nd[kGva][4][16][16];   // diagonal blocks N_aa, column-major: nd[a][column][row]
-  float td[kGva][4][16][16];   // their inverses T_aa, column-major
-};
-
-union PrepassSmem {
-  PrepassWaveSmem w[kPrepassWaves];
-  int plan[kPlanScratch];      // planner scratch (work-group 0 of a fused launch)
+  // diagonal blocks N_aa, column-major (nt[a][column][row]); the forward
+  // substitution then overwrites each with its inverse T_aa (a wave reads all of
+  // its N columns before its first T store)
+  float nt[kGva][4][16][16];
 };
 
 // Batches of at most kFusedPlanSeqs sequences number their records inside the
-// prepass (no plan launch): every wave scans the chunk counts of all sequences
-// once (64 per lane block) and finds each item's sequence with a ballot.
+// prepass (no plan launch): wave 0 of each work-group scans the chunk counts
+// of all sequences once into LDS, and each item finds its sequence there with
+// a ballot.
 constexpr int kFusedPlanSeqs = 512;
 constexpr int kFusedBlocks = kFusedPlanSeqs / 64;
+
+struct PrepassSeqSmem {
+  int incl[kFusedPlanSeqs];          // inclusive prefix of the chunk counts (past the last: the total)
+  long long s0[kFusedPlanSeqs];      // sequence bounds (clamped)
+  long long s1[kFusedPlanSeqs];
+};
+
+struct PrepassSmem {
+  union {
+    PrepassWaveSmem w[kPrepassWaves];
+    int plan[kPlanScratch];      // planner scratch (work-group 0 of a fused launch)
+  } u;
+  PrepassSeqSmem seq;
+};
+
 
 // acc + X Y for 16x16 fp32 blocks with X^T and Y in C layout (lane (lg, l16),
 // register r: row 4 lg + r, column l16), on two bf16 MFMAs with both operands
@@ -882,7 +894,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr)
             if (l16 == 4 * lg + rr) kb[e] += __log2f(fmaxf(1.0f, fabsf(1.0f - brow[e][m][rr] * kk[m][m][rr])));
-          *reinterpret_cast<f32x4*>(&ws.nd[e][m][l16][4 * lg]) = nv;
+          *reinterpret_cast<f32x4*>(&ws.nt[e][m][l16][4 * lg]) = nv;
         } else {
           nlo[e][m][n] = nv;
         }
@@ -894,17 +906,21 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
   // ---- T_aa = (I + N_aa)^{-1} by forward substitution: lane (a = lg, j = l16)
   // forms column j of T_aa; once x[i] is final every later row subtracts
   // N[r][i] x[i] (the row-wise recurrence's terms and order, dependency depth 16) ----
+  // the column index through an opaque move: otherwise the compiler hoists the
+  // identity columns out of the item loop and spills them
+  int jcol;
+  asm volatile("v_and_b32 %0, 15, %1" : "=v"(jcol) : "v"(lane));
 #pragma unroll
   for (int e = 0; e < NH; ++e) {
     float x[16];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = i == l16 ? 1.0f : 0.0f;
+    for (int i = 0; i < 16; ++i) x[i] = i == jcol ? 1.0f : 0.0f;
 #pragma unroll
     for (int i = 0; i < 15; ++i) {
       float col[16];
 #pragma unroll
       for (int qv = (i + 1) >> 2; qv < 4; ++qv) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(&ws.nd[e][lg][i][4 * qv]);
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(&ws.nt[e][lg][i][4 * qv]);
 #pragma unroll
         for (int u = 0; u < 4; ++u) col[4 * qv + u] = v4[u];
       }
@@ -913,7 +929,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     }
 #pragma unroll
     for (int qv = 0; qv < 4; ++qv)
-      *reinterpret_cast<f32x4*>(&ws.td[e][lg][l16][4 * qv]) = f32x4{x[4 * qv], x[4 * qv + 1], x[4 * qv + 2], x[4 * qv + 3]};
+      *reinterpret_cast<f32x4*>(&ws.nt[e][lg][l16][4 * qv]) = f32x4{x[4 * qv], x[4 * qv + 1], x[4 * qv + 2], x[4 * qv + 3]};
   }
   wave_lds_sync();
 
@@ -926,9 +942,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     f32x4 tc[4], w[4][4];   // tc[a] = T_aa = (W_aa)^T in C layout; w[a][b] = W_ab, a <= b
 #pragma unroll
     for (int ab = 0; ab < 4; ++ab) {
-      tc[ab] = *reinterpret_cast<const f32x4*>(&ws.td[e][ab][l16][4 * lg]);
+      tc[ab] = *reinterpret_cast<const f32x4*>(&ws.nt[e][ab][l16][4 * lg]);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) w[ab][ab][rr] = ws.td[e][ab][4 * lg + rr][l16];
+      for (int rr = 0; rr < 4; ++rr) w[ab][ab][rr] = ws.nt[e][ab][4 * lg + rr][l16];
     }
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -969,6 +985,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
   }
 }
 
+template <bool kPair>
 __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const float* __restrict__ A_log, const uint16_t* __restrict__ a,
@@ -981,45 +998,37 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     // work-group 0 plans the batch (lists for the consumer) while the others
     // run the records
     int total_recs;
-    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, sm.plan, total_recs);
+    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, sm.u.plan, total_recs);
     return;
   }
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-  PrepassWaveSmem& ws = sm.w[wv];
+  PrepassWaveSmem& ws = sm.u.w[wv];
   const int gw = (static_cast<int>(blockIdx.x) - fused_plan) * kPrepassWaves + wv;
   const int nw = (static_cast<int>(gridDim.x) - fused_plan) * kPrepassWaves;
 
-  // records: small batches scan the chunk counts here (lane l of block j owns
-  // sequence 64 j + l); incl = inclusive prefix of the chunk counts.  The
-  // bounds of block 0's sequences stay in registers.
-  int incl[kFusedBlocks];
-  long long b0s0 = 0, b0s1 = 0;
+  // records: small batches scan the chunk counts here (wave 0; lane l of block
+  // j owns sequence 64 j + l), into LDS
   int total;
   if (fused_plan) {
-    int carry = 0;
-#pragma unroll
-    for (int j = 0; j < kFusedBlocks; ++j) {
-      int nch = 0;
-      if (64 * j < num_seqs) {
+    const int nblk = (num_seqs + 63) / 64;
+    if (wv == 0) {
+      int carry = 0;
+      for (int j = 0; j < nblk; ++j) {
         const int s = 64 * j + lane;
-        if (s < num_seqs) {
-          long long t0, t1;
-          seq_bounds(cu, is64, s, T, t0, t1);
-          nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
-          if (j == 0) {
-            b0s0 = t0;
-            b0s1 = t1;
-          }
-        }
-        incl[j] = wave_incl_sum(nch) + carry;
-        carry = __builtin_amdgcn_readlane(incl[j], 63);
-      } else {
-        incl[j] = carry;
+        long long t0 = 0, t1 = 0;
+        if (s < num_seqs) seq_bounds(cu, is64, s, T, t0, t1);
+        const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
+        const int inc = wave_incl_sum(nch) + carry;
+        sm.seq.incl[s] = inc;
+        sm.seq.s0[s] = t0;
+        sm.seq.s1[s] = t1;
+        carry = __builtin_amdgcn_readlane(inc, 63);
       }
     }
-    total = min(carry, R);
+    __syncthreads();
+    total = min(sm.seq.incl[64 * nblk - 1], R);
   } else {
     total = min(rec_start[num_seqs], R);
   }
@@ -1027,7 +1036,7 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
   // items: (record r, v-head h) = 8 r + h, or (record r, q/k head hq) = 4 r + hq
   // with both v-heads of the pair; consecutive items share a work-group, so the
   // waves that read the same K / Q rows go through one L2
-  const bool pair_items = static_cast<long long>(total) * kVHeads > kPrepassResident;
+  constexpr bool pair_items = kPair;
   const int per_rec = pair_items ? kQKHeads : kVHeads;
   const int nitems = total * per_rec;
   for (int item = gw; item < nitems; item += nw) {
@@ -1037,33 +1046,20 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     const int ne = pair_items ? kGva : 1;
     long long t0, s1;
     if (fused_plan) {
+      // the first sequence whose inclusive chunk count exceeds r (one exists: r < total)
       int s = 0, start = 0;
-      bool found = false;
-#pragma unroll
-      for (int j = 0; j < kFusedBlocks; ++j) {
-        if (!found && 64 * j < num_seqs) {
-          const unsigned long long m = __builtin_amdgcn_ballot_w64(incl[j] > r);
-          if (m != 0) {
-            const int l = static_cast<int>(__builtin_ctzll(m));
-            s = 64 * j + l;
-            start = l > 0 ? __builtin_amdgcn_readlane(incl[j], l - 1)
-                          : (j > 0 ? __builtin_amdgcn_readlane(incl[j > 0 ? j - 1 : 0], 63) : 0);
-            found = true;
-          }
+      for (int j = 0;; ++j) {
+        const int inc = sm.seq.incl[64 * j + lane];
+        const unsigned long long m = __builtin_amdgcn_ballot_w64(inc > r);
+        if (m != 0) {
+          const int l = static_cast<int>(__builtin_ctzll(m));
+          s = 64 * j + l;
+          start = s > 0 ? __builtin_amdgcn_readfirstlane(sm.seq.incl[s - 1]) : 0;
+          break;
         }
       }
-      long long s0;
-      if (s < 64) {
-        const unsigned long long x0 = static_cast<unsigned long long>(b0s0), x1 = static_cast<unsigned long long>(b0s1);
-        s0 = static_cast<long long>(
-            (static_cast<unsigned long long>(static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x0 >> 32), s))) << 32) |
-            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x0 & 0xffffffffu), s)));
-        s1 = static_cast<long long>(
-            (static_cast<unsigned long long>(static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x1 >> 32), s))) << 32) |
-            static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(x1 & 0xffffffffu), s)));
-      } else {
-        seq_bounds(cu, is64, s, T, s0, s1);
-      }
+      const long long s0 = sm.seq.s0[s];
+      s1 = sm.seq.s1[s];
       t0 = s0 + static_cast<long long>(r - start) * kChunk;
     } else {
       const int4 rec = recs[r];
@@ -1084,35 +1080,41 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
       a_t[e] = e < ne ? bf2f(a[gi + e]) : 0.0f;
       b_t[e] = e < ne ? bf2f(b[gi + e]) : 0.0f;
     }
-    bf16x8 kf[4][4], qf[4][4];
+    const uint16_t* krow[4];
+    const uint16_t* qrow[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
-      const uint16_t* kr = k + (row * kQKHeads + hq) * kDim + 8 * lg;
-      const uint16_t* qr = q + (row * kQKHeads + hq) * kDim + 8 * lg;
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        kf[m][d] = *reinterpret_cast<const bf16x8*>(kr + 32 * d);
-        qf[m][d] = *reinterpret_cast<const bf16x8*>(qr + 32 * d);
-      }
+      krow[m] = k + (row * kQKHeads + hq) * kDim + 8 * lg;
+      qrow[m] = q + (row * kQKHeads + hq) * kDim + 8 * lg;
     }
 
     // ---- raw grams, shared by the v-heads of the pair: kk = K K^T (lower
     // tiles), qk = K Q^T (upper tiles, i.e. Q K^T transposed) ----
     f32x4 kk[4][4], qk[4][4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < 4; ++m)
 #pragma unroll
-      for (int n = 0; n <= m; ++n) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f}, acq = {0.f, 0.f, 0.f, 0.f};
+      for (int n = 0; n <= m; ++n) kk[m][n] = qk[n][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
+      // all of the rows' fragments in flight at once
+      bf16x8 kf[4][4], qf[4][4];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int dd = 0; dd < 4; ++dd) {
-          acc = mfma16(kf[m][dd], kf[n][dd], acc);
-          acq = mfma16(kf[n][dd], qf[m][dd], acq);
+          kf[dd][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
+          qf[dd][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
         }
-        kk[m][n] = acc;
-        qk[n][m] = acq;
-      }
+#pragma unroll
+      for (int dd = 0; dd < 4; ++dd)
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+          for (int n = 0; n <= m; ++n) {
+            kk[m][n] = mfma16(kf[dd][m], kf[dd][n], kk[m][n]);
+            qk[n][m] = mfma16(kf[dd][n], qf[dd][m], qk[n][m]);
+          }
     }
 
     const int h0 = kGva * hq + e0;
@@ -1124,10 +1126,14 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     }
     uint16_t* frag0 = ws_frag + (static_cast<size_t>(r) * kVHeads + h0) * kFrags * kMatElems;
     float* gp0 = ws_gam + (static_cast<size_t>(r) * kVHeads + h0) * kGamStride;
-    if (pair_items)
-      prepass_heads<kGva>(ws, kk, qk, c, a_t, b_t, alog, dtb, frag0, gp0);
-    else
-      prepass_heads<1>(ws, kk, qk, c, a_t, b_t, alog, dtb, frag0, gp0);
+    // the v-heads of a pair one after the other (interleaving their phases
+    // gains nothing: the phases are VALU-bound, not latency-bound)
+    for (int e = 0; e < ne; ++e) {
+      const float a1[kGva] = {e == 0 ? a_t[0] : a_t[1], 0.0f}, b1[kGva] = {e == 0 ? b_t[0] : b_t[1], 0.0f};
+      const float al1[kGva] = {e == 0 ? alog[0] : alog[1], 0.0f}, dt1[kGva] = {e == 0 ? dtb[0] : dtb[1], 0.0f};
+      prepass_heads<1>(ws, kk, qk, c, a1, b1, al1, dt1, frag0 + e * static_cast<size_t>(kFrags) * kMatElems,
+                       gp0 + e * kGamStride);
+    }
   }
 }
 
@@ -2452,13 +2458,21 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
   if (!fused_plan)
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                         total_tokens, Ri, gc, rec_start, recs, lists);
-  // one wave per (record, v-head), or per (record, q/k head) when those would
-  // not all be resident at once; at most two work-groups per CU
-  const long long pre_items = R * kVHeads > kPrepassResident ? R * kQKHeads : R * kVHeads;
-  const long long g_pre = std::min<long long>((pre_items + kPrepassWaves - 1) / kPrepassWaves, kPrepassMaxGroups);
-  prepass_kernel<<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
-      qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
-      Ri, gc, fused_plan, rec_start, lists, frag, gam);
+  // one wave per (record, v-head) for small batches (a lone item's latency
+  // matters there), else one per (record, q/k head): then the grams and the K /
+  // Q loads are not repeated per v-head, and up to 512 records start at once
+  if (R * kVHeads <= kPrepassMaxGroups * kPrepassWaves) {
+    const long long g_pre = (R * kVHeads + kPrepassWaves - 1) / kPrepassWaves;
+    prepass_kernel<false><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
+        qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
+        Ri, gc, fused_plan, rec_start, lists, frag, gam);
+  } else {
+    const long long g_pre =
+        std::min<long long>((R * kQKHeads + kPrepassWaves - 1) / kPrepassWaves, kPrepassMaxGroups);
+    prepass_kernel<true><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
+        qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
+        Ri, gc, fused_plan, rec_start, lists, frag, gam);
+  }
   // persistent grids: one work-group per CU per consumer kind at most; a
   // sequence needs 2 chunks (65 tokens) to be long
   const long long g_long =
