@@ -1655,14 +1655,18 @@ __device__ __forceinline__ void state_frags(const f32x4 (&st)[8], bf16x8 (&sb)[4
   }
 }
 
-// Same fragments as a bf16 hi + lo pair (lo = bf16 of the rounding residue).
-__device__ __forceinline__ void state_frags_hilo(const f32x4 (&st)[8], bf16x8 (&hi)[4], bf16x8 (&lo)[4]) {
+// The bf16 rounding residues of those fragments (lo = bf16(x - hi)).
+__device__ __forceinline__ void state_frags_lo(const f32x4 (&st)[8], const bf16x8 (&hi)[4], bf16x8 (&lo)[4]) {
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
-    float x[8];
+    const u32x4 h = __builtin_bit_cast(u32x4, hi[d]);
+    u32x4 l;
 #pragma unroll
-    for (int s = 0; s < 8; ++s) x[s] = st[2 * d + (s >> 2)][s & 3];
-    split_frag(x, hi[d], lo[d]);
+    for (int j = 0; j < 4; ++j) {
+      const int s = 2 * j;
+      l[j] = pack_bf2(st[2 * d + (s >> 2)][s & 3] - bf_lo(h[j]), st[2 * d + ((s + 1) >> 2)][(s + 1) & 3] - bf_hi(h[j]));
+    }
+    lo[d] = __builtin_bit_cast(bf16x8, l);
   }
 }
 
@@ -1677,13 +1681,41 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   const int vrow = 4 * lg + (l16 >> 2);
   const int vat = 8 * ((2 * w + ((l16 & 3) >> 1)) ^ vh_swz(vrow)) + 4 * (l16 & 1);
 
-  // ---- operands of X = K S^T and R = V - gam X ----
+  // ---- X = K S^T.  S enters as one bf16, plus its bf16 rounding residue
+  // in a second pass when the chunk's map bound says the state barely decays:
+  // then the rounding of S here is what accumulates over a long sequence
+  // (single bf16: state error 1.2e-3 to 1.5e-3 at 4k to 28k tokens of near-1
+  // decay; hi + lo: 3e-4 to 4e-4).  Where the map contracts by 2^-8 or more
+  // per chunk, earlier roundings do not accumulate and one bf16 suffices.
+  // The K fragments are read in two batches of eight and the products of a
+  // depth chunk start once its fragments have landed (at most 15 LDS reads
+  // can be waited for individually); the bound, read first, is tested after
+  // the first pass.
+  const float cbound = sm.gt[P][kBoundAt];   // first LDS read: done before the first K fragment
   bf16x8 ka[4][4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d)
+  auto read_k = [&](int d) {
 #pragma unroll
     for (int m = 0; m < 4; ++m)
       ka[d][m] = *reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]);
+  };
+  read_k(0);
+  read_k(1);
+  bf16x8 sb[4];
+  state_frags(st, sb);
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 X[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[0][m], sb[0], f32x4{0.f, 0.f, 0.f, 0.f});
+  __builtin_amdgcn_sched_barrier(0);
+  read_k(2);
+  read_k(3);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[1][m], sb[1], X[m]);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[2][m], sb[2], X[m]);
+  __builtin_amdgcn_sched_barrier(0);
+  // operands of R = V - gam X and the chunk's map bound
   f32x4 gam[4];
   u32x2 vw[4];
 #pragma unroll
@@ -1691,34 +1723,16 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
     gam[m] = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
     vw[m] = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
   }
-  // ---- X = K S^T.  S enters as one bf16, or as a bf16 hi + lo pair when
-  // the chunk's map bound says the state barely decays: then the rounding of
-  // S here is what accumulates over a long sequence (single bf16: state error
-  // 1.2e-3 to 1.5e-3 at 4k to 28k tokens of near-1 decay; hi + lo: 3e-4 to
-  // 4e-4).  Where the map contracts by 2^-8 or more per chunk, earlier
-  // roundings do not accumulate and one bf16 suffices. ----
-  bf16x8 sb[4];
-  f32x4 X[4];
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int m = 0; m < 4; ++m) X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (sm.gt[P][kBoundAt] > kHiLoBoundLog2) {   // uniform
+  for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[3][m], sb[3], X[m]);
+  if (cbound > kHiLoBoundLog2) {   // uniform
     bf16x8 sbl[4];
-    state_frags_hilo(st, sb, sbl);
-    __builtin_amdgcn_sched_barrier(0);
+    state_frags_lo(st, sb, sbl);
 #pragma unroll
     for (int d = 0; d < 4; ++d)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        X[m] = mfma16(ka[d][m], sbl[d], X[m]);
-        X[m] = mfma16(ka[d][m], sb[d], X[m]);
-      }
-  } else {
-    state_frags(st, sb);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-#pragma unroll
-      for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[d][m], sb[d], X[m]);
+      for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[d][m], sbl[d], X[m]);
   }
   // Tb fragments land while X runs
   f16x8 tb[2][4];
