@@ -280,6 +280,29 @@ def chain_step_us(args, torch, dev) -> dict:
             "method": "(t(1 x 256 tokens) - t(1 x 128 tokens)) / 2, warm cache"}
 
 
+# Prefill workloads beside the three configurations: configuration 3 with
+# near-1 decay (every chunk takes the state's bf16 lo pass, and the segment
+# maps stay large), and one-sequence prompts shorter than a chunk and of one
+# chunk, where a call is launch-bound.
+EXTRA_PREFILL = ("c3_slow_decay", "t16", "t64")
+
+
+def extra_prefill_inputs(name):
+    import torch
+
+    from kachua_mlsys_amd.inputs import prefill_config, prefill_inputs_from_lengths
+
+    if name == "c3_slow_decay":
+        p = prefill_config(3)
+        p.A_log = torch.linspace(-8.0, -5.0, 8)
+        return p
+    if name == "t16":
+        return prefill_inputs_from_lengths([16], seed=16)
+    if name == "t64":
+        return prefill_inputs_from_lengths([64], seed=64)
+    raise ValueError(f"unknown extra prefill workload {name!r} (known: {', '.join(EXTRA_PREFILL)})")
+
+
 # Prefill shapes the reference published B200 timings for (contest workloads;
 # the varlen lengths live in the contest dataset, which is not available
 # offline: those use this build's seeded log-uniform lengths at the same T, N).
@@ -320,6 +343,9 @@ def main():
     ap.add_argument("--warm-cache", action="store_true", help="do not rotate buffers")
     ap.add_argument("--prefill-configs", default="3,2,4",
                     help="comma-separated prefill configurations to time (for profiling)")
+    ap.add_argument("--prefill-extra", default=None,
+                    help="comma-separated extra prefill workloads (" + ", ".join(EXTRA_PREFILL) +
+                         "); default all of them, none with --profile")
     ap.add_argument("--profile", action="store_true",
                     help="time only the named workloads (no chain-step, warm-cache or bandwidth-probe "
                          "launches), so counter runs see one workload per kernel")
@@ -414,6 +440,15 @@ def main():
             if cfg == 3 and not args.no_cpu:
                 entry["cpu_baseline"] = cpu_prefill_baseline(torch, p_cpu)
             pre[f"c{cfg}"] = entry
+        extra = args.prefill_extra
+        if extra is None:
+            extra = "" if args.profile else ",".join(EXTRA_PREFILL)
+        for name in (x.strip() for x in extra.split(",") if x.strip()):
+            p_cpu = extra_prefill_inputs(name)
+            e = time_prefill(p_cpu, args, torch, dev, warm=name != "c3_slow_decay")
+            pre[name] = {k: e[k] for k in ("tokens", "seqs", "max_len", "us_per_call",
+                                           "us_per_call_eager_python_loop", "tokens_per_s", "cache")}
+            pre[name]["roofline_frac"] = e["roofline"]["frac"]
         if step is not None:
             pre["chain_step"] = step
         result["prefill"] = pre

@@ -18,10 +18,12 @@
 //              records, segment length and work lists from cu_seqlens.  For
 //              smaller batches work-group 0 of the prepass plans and the other
 //              prepass work-groups find their own records.
-//   prepass  : one work-group per (record, q/k head), all records in
-//              parallel: gates, K K^T / Q K^T on MFMA, fp32 blocked triangular
-//              inverse, and the packed MFMA operands Tb (fp16), Aqk (bf16) plus
-//              gam / tail, written to the workspace.
+//   prepass  : one wave per (record, v-head), or per (record, q/k head) for
+//              large batches, all records in parallel: gates, K K^T / Q K^T on
+//              MFMA, the blocked triangular inverse (diagonal blocks by fp32
+//              forward substitution, the rest on MFMA with bf16 hi + lo
+//              operands), and the packed MFMA operands Tb (fp16), Aqk (bf16)
+//              plus gam / tail, written to the workspace.
 //   consumer : persistent work-groups.  Long sequences are cut into segments
 //              of L chunks (L chosen by the plan); every segment runs at once,
 //              segments >= 1 twice (zero initial state with the real V, and
@@ -35,11 +37,14 @@
 //              final state of multi-segment sequences.
 //
 // Precision policy (fp32 accumulation everywhere): K, Q, V are bf16 inputs, so
-// their products are exact.  S enters K S^T and Q S^T as a single bf16; Tb and
+// their products are exact.  S enters Q S^T as a single bf16 and K S^T as a
+// single bf16, or as a bf16 hi + lo pair in chunks whose map bound shows slow
+// decay (the state's rounding then survives many chunks); Tb and
 // R = V - gam K S^T enter Delta = Tb R as fp16 (11 significant bits: one MFMA
-// instead of three for a bf16 hi+lo pair); the state update uses
-// Delta' = tail Delta as a bf16 hi+lo pair; Aqk Delta (output only) is single
-// bf16.  The fp32 state never leaves registers between chunks.
+// instead of three for a bf16 hi+lo pair), R scaled by a power of two into
+// fp16's normal range first; the state update uses Delta' = tail Delta as a
+// bf16 hi+lo pair; Aqk Delta (output only) is single bf16.  The fp32 state
+// never leaves registers between chunks.
 #include "gdn_common.h"
 #include <algorithm>
 #include <atomic>
