@@ -782,20 +782,29 @@ struct PrepassSmem {
 // register r: row 4 lg + r, column l16), on two bf16 MFMAs with both operands
 // split into bf16 hi + lo: X_hi Y_hi + X_lo Y_hi + X_hi Y_lo (relative error
 // about 2^-16, far below the fp16 rounding of Tb).  Depth slot s of lane group
-// lg is product depth 4 lg + (s & 3): slots 0-3 pair X_hi with Y_hi, slots 4-7
-// X_lo with Y_hi in the first MFMA and X_hi with Y_lo... as 0 x lo in the
-// second, where slots 4-7 of B are zero.
-__device__ __forceinline__ f32x4 prod16(const f32x4& xt, const f32x4& y, f32x4 acc) {
+// lg is product depth 4 lg + (s & 3): the A operand holds X_hi in slots 0-3
+// and X_lo in slots 4-7; the first B operand holds Y_hi in both halves, the
+// second Y_lo in slots 0-3 and zeros in 4-7.  An operand used in several
+// products is split once.
+__device__ __forceinline__ bf16x8 split_x(const f32x4& xt) {
   const uint32_t xh0 = pack_bf2(xt[0], xt[1]), xh1 = pack_bf2(xt[2], xt[3]);
   const uint32_t xl0 = pack_bf2(xt[0] - bf_lo(xh0), xt[1] - bf_hi(xh0));
   const uint32_t xl1 = pack_bf2(xt[2] - bf_lo(xh1), xt[3] - bf_hi(xh1));
+  return __builtin_bit_cast(bf16x8, u32x4{xh0, xh1, xl0, xl1});
+}
+struct YSplit {
+  bf16x8 hh, l0;
+};
+__device__ __forceinline__ YSplit split_y(const f32x4& y) {
   const uint32_t yh0 = pack_bf2(y[0], y[1]), yh1 = pack_bf2(y[2], y[3]);
   const uint32_t yl0 = pack_bf2(y[0] - bf_lo(yh0), y[1] - bf_hi(yh0));
   const uint32_t yl1 = pack_bf2(y[2] - bf_lo(yh1), y[3] - bf_hi(yh1));
-  const bf16x8 xa = __builtin_bit_cast(bf16x8, u32x4{xh0, xh1, xl0, xl1});
-  acc = mfma16(xa, __builtin_bit_cast(bf16x8, u32x4{yh0, yh1, yh0, yh1}), acc);
-  acc = mfma16(xa, __builtin_bit_cast(bf16x8, u32x4{yl0, yl1, 0u, 0u}), acc);
-  return acc;
+  return YSplit{__builtin_bit_cast(bf16x8, u32x4{yh0, yh1, yh0, yh1}),
+                __builtin_bit_cast(bf16x8, u32x4{yl0, yl1, 0u, 0u})};
+}
+__device__ __forceinline__ f32x4 prod16(const bf16x8& xa, const YSplit& y, f32x4 acc) {
+  acc = mfma16(xa, y.hh, acc);
+  return mfma16(xa, y.l0, acc);
 }
 
 // Wave-local LDS hand-off between lanes of one wave: LDS operations of a wave
@@ -869,8 +878,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
             x[4 * hf + rr] = (ai <= m && i <= t) ? fast_exp2(lcol[e][m] - lrow[e][ai][rr]) * qk[ai][m][rr] : 0.0f;
           }
         }
-        *reinterpret_cast<u32x4*>(frag0 + e * kFragStride + kMatElems + (frag_slot(m, d) * 64 + lane) * 8) =
-            u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])};
+        __builtin_nontemporal_store(
+            u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])},
+            reinterpret_cast<u32x4*>(frag0 + e * kFragStride + kMatElems + (frag_slot(m, d) * 64 + lane) * 8));
       }
     }
   }
@@ -920,17 +930,25 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = i == jcol ? 1.0f : 0.0f;
+    // column i's quads are read three steps ahead into a ring (at most 12 LDS
+    // reads in flight), so a step waits only for reads issued long before it
+    // instead of one LDS round trip per step
+    constexpr int kAhead = 3;
+    f32x4 ring[kAhead][4];
+    auto read_col = [&](int i, f32x4 (&c)[4]) {
+#pragma unroll
+      for (int qv = (i + 1) >> 2; qv < 4; ++qv) c[qv] = *reinterpret_cast<const f32x4*>(&ws.nt[e][lg][i][4 * qv]);
+    };
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i) read_col(i, ring[i]);
 #pragma unroll
     for (int i = 0; i < 15; ++i) {
-      float col[16];
+      f32x4 (&c)[4] = ring[i % kAhead];
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int qv = (i + 1) >> 2; qv < 4; ++qv) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(&ws.nt[e][lg][i][4 * qv]);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) col[4 * qv + u] = v4[u];
-      }
-#pragma unroll
-      for (int rr = i + 1; rr < 16; ++rr) x[rr] = fmaf(-col[rr], x[i], x[rr]);
+      for (int rr = i + 1; rr < 16; ++rr) x[rr] = fmaf(-c[rr >> 2][rr & 3], x[i], x[rr]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + kAhead < 15) read_col(i + kAhead, ring[i % kAhead]);
     }
 #pragma unroll
     for (int qv = 0; qv < 4; ++qv)
@@ -952,16 +970,30 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
       for (int rr = 0; rr < 4; ++rr) w[ab][ab][rr] = ws.nt[e][ab][4 * lg + rr][l16];
     }
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    // operands split once: tx[a] from T_aa, nx[m][a] from N_ma = U_am^T,
+    // wy[m][b] from W_mb (m >= 1: the rows above use it)
+    bf16x8 tx[3], nx[4][3];
+    YSplit wy[4][4];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) tx[a] = split_x(tc[a]);
+#pragma unroll
+    for (int m = 1; m < 4; ++m) {
+      wy[m][m] = split_y(w[m][m]);
+#pragma unroll
+      for (int a = 0; a < m; ++a) nx[m][a] = split_x(nlo[e][m][a]);
+    }
 #pragma unroll
     for (int dist = 1; dist < 4; ++dist) {
 #pragma unroll
       for (int ab = 0; ab + dist < 4; ++ab) {
         const int bb = ab + dist;
-        // P = sum_m U_am W_mb with U_am^T = N_ma (C layout)
-        f32x4 p = prod16(nlo[e][ab + 1][ab], w[ab + 1][bb], z4);
-        if (dist >= 2) p = prod16(nlo[e][ab + 2][ab], w[ab + 2][bb], p);
-        if (dist >= 3) p = prod16(nlo[e][ab + 3][ab], w[ab + 3][bb], p);
-        w[ab][bb] = -prod16(tc[ab], p, z4);
+        // P = sum_m U_am W_mb, the term of the block formed last (m = ab + 1)
+        // added last, so only it waits for the previous distance
+        f32x4 p = z4;
+#pragma unroll
+        for (int m = bb; m > ab; --m) p = prod16(nx[m][ab], wy[m][bb], p);
+        w[ab][bb] = -prod16(tx[ab], split_y(p), z4);
+        if (ab >= 1) wy[ab][bb] = split_y(w[ab][bb]);
       }
     }
 #pragma unroll
@@ -976,8 +1008,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = ai <= m ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
         }
-        *reinterpret_cast<u32x4*>(frag0 + e * kFragStride + (frag_slot(m, d) * 64 + lane) * 8) =
-            u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])};
+        __builtin_nontemporal_store(
+            u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])},
+            reinterpret_cast<u32x4*>(frag0 + e * kFragStride + (frag_slot(m, d) * 64 + lane) * 8));
       }
     }
   }
@@ -1102,24 +1135,30 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
 #pragma unroll
       for (int n = 0; n <= m; ++n) kk[m][n] = qk[n][m] = f32x4{0.f, 0.f, 0.f, 0.f};
     {
-      // all of the rows' fragments in flight at once
-      bf16x8 kf[4][4], qf[4][4];
+      // the rows' fragments by depth chunk, two chunks in flight: chunk dd + 2
+      // is loaded into chunk dd's registers once its products are issued
+      // (half the operand registers of loading all four at once)
+      bf16x8 kf[2][4], qf[2][4];
+      auto load_dd = [&](int dd) {
 #pragma unroll
-      for (int m = 0; m < 4; ++m)
-#pragma unroll
-        for (int dd = 0; dd < 4; ++dd) {
-          kf[dd][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
-          qf[dd][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
+        for (int m = 0; m < 4; ++m) {
+          kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
+          qf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
         }
+      };
+      load_dd(0);
+      load_dd(1);
 #pragma unroll
-      for (int dd = 0; dd < 4; ++dd)
+      for (int dd = 0; dd < 4; ++dd) {
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
           for (int n = 0; n <= m; ++n) {
-            kk[m][n] = mfma16(kf[dd][m], kf[dd][n], kk[m][n]);
-            qk[n][m] = mfma16(kf[dd][n], qf[dd][m], qk[n][m]);
+            kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
+            qk[n][m] = mfma16(kf[dd & 1][n], qf[dd & 1][m], qk[n][m]);
           }
+        if (dd + 2 < 4) load_dd(dd + 2);
+      }
     }
 
     const int h0 = kGva * hq + e0;
