@@ -815,12 +815,25 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// One lane's 16 bytes of a fragment: streamed to global memory (read once, by
+// the consumer), or a plain LDS store.
+template <bool kToLds>
+__device__ __forceinline__ void store_frag(const u32x4& x, uint16_t* dst) {
+  if constexpr (kToLds) {
+    *reinterpret_cast<u32x4*>(dst) = x;
+  } else {
+    __builtin_nontemporal_store(x, reinterpret_cast<u32x4*>(dst));
+  }
+}
+
 // The terms of NH v-heads (one, or both of a GVA pair, interleaved phase by
 // phase so that their independent latency chains overlap) from the chunk's raw
 // grams: kk[m][n] (n <= m) holds [t = 16 m + 4 lg + rr][i = 16 n + l16] =
 // k_t . k_i; qk[a][m] (a <= m) holds [i = 16 a + 4 lg + rr][t = 16 m + l16] =
 // k_i . q_t.  a_t, b_t: this lane's token (clamped into the chunk) per v-head.
-template <int NH>
+// The terms go to frag0 / gp0 in the workspace layout: global memory
+// (streamed out), or LDS when kToLds (the direct path).
+template <int NH, bool kToLds = false>
 __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4], const f32x4 (&qk)[4][4],
                                               int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
                                               const float (&alog)[kGva], const float (&dtb)[kGva],
@@ -878,9 +891,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
             x[4 * hf + rr] = (ai <= m && i <= t) ? fast_exp2(lcol[e][m] - lrow[e][ai][rr]) * qk[ai][m][rr] : 0.0f;
           }
         }
-        __builtin_nontemporal_store(
+        store_frag<kToLds>(
             u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])},
-            reinterpret_cast<u32x4*>(frag0 + e * kFragStride + kMatElems + (frag_slot(m, d) * 64 + lane) * 8));
+            frag0 + e * kFragStride + kMatElems + (frag_slot(m, d) * 64 + lane) * 8);
       }
     }
   }
@@ -1008,9 +1021,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = ai <= m ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
         }
-        __builtin_nontemporal_store(
+        store_frag<kToLds>(
             u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])},
-            reinterpret_cast<u32x4*>(frag0 + e * kFragStride + (frag_slot(m, d) * 64 + lane) * 8));
+            frag0 + e * kFragStride + (frag_slot(m, d) * 64 + lane) * 8);
       }
     }
   }
@@ -1020,6 +1033,55 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
   for (int e = 0; e < NH; ++e) {
     const float lb = wave_sumf(kb[e]) + last[e];
     if (lane == 0) gp0[e * kGamStride + kBoundAt] = lb;
+  }
+}
+
+// Raw grams of one chunk (rows t0 .. t0 + c - 1 of q/k head hq), one wave:
+// kk = K K^T (lower tiles, kk[m][n] = [t = 16 m + 4 lg + rr][i = 16 n + l16]),
+// qk = K Q^T (upper tiles, qk[n][m] = [i = 16 n + 4 lg + rr][t = 16 m + l16]).
+// Fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
+// columns 32 d + 8 lg .. + 7.  Rows past the chunk end repeat row c - 1: they
+// meet beta = 0 (rows of N), i <= t masks and output rows never stored.
+__device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                            long long t0, int c, int hq, int lane, f32x4 (&kk)[4][4],
+                                            f32x4 (&qk)[4][4]) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int cm1 = c - 1;
+  const uint16_t* krow[4];
+  const uint16_t* qrow[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
+    krow[m] = k + (row * kQKHeads + hq) * kDim + 8 * lg;
+    qrow[m] = q + (row * kQKHeads + hq) * kDim + 8 * lg;
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int n = 0; n <= m; ++n) kk[m][n] = qk[n][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // the rows' fragments by depth chunk, two chunks in flight: chunk dd + 2 is
+  // loaded into chunk dd's registers once its products are issued (half the
+  // operand registers of loading all four at once)
+  bf16x8 kf[2][4], qf[2][4];
+  auto load_dd = [&](int dd) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
+      qf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
+    }
+  };
+  load_dd(0);
+  load_dd(1);
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int n = 0; n <= m; ++n) {
+        kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
+        qk[n][m] = mfma16(kf[dd & 1][n], qf[dd & 1][m], qk[n][m]);
+      }
+    if (dd + 2 < 4) load_dd(dd + 2);
   }
 }
 
@@ -1107,10 +1169,8 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     const int c = static_cast<int>(min(static_cast<long long>(kChunk), s1 - t0));
     const int cm1 = c - 1;
 
-    // ---- loads: gates (lane = token), K / Q rows as MFMA fragments ----
-    // fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
-    // columns 32 d + 8 lg .. + 7.  Rows past the chunk end repeat row c - 1:
-    // they meet beta = 0 (rows of N), i <= t masks and output rows never stored.
+    // ---- loads: gates (lane = token, clamped into the chunk), then the raw
+    // grams, shared by the v-heads of the pair ----
     const size_t gi = static_cast<size_t>(t0 + min(lane, cm1)) * kVHeads + kGva * hq + e0;
     float a_t[kGva], b_t[kGva];
 #pragma unroll
@@ -1118,48 +1178,8 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
       a_t[e] = e < ne ? bf2f(a[gi + e]) : 0.0f;
       b_t[e] = e < ne ? bf2f(b[gi + e]) : 0.0f;
     }
-    const uint16_t* krow[4];
-    const uint16_t* qrow[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
-      krow[m] = k + (row * kQKHeads + hq) * kDim + 8 * lg;
-      qrow[m] = q + (row * kQKHeads + hq) * kDim + 8 * lg;
-    }
-
-    // ---- raw grams, shared by the v-heads of the pair: kk = K K^T (lower
-    // tiles), qk = K Q^T (upper tiles, i.e. Q K^T transposed) ----
     f32x4 kk[4][4], qk[4][4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int n = 0; n <= m; ++n) kk[m][n] = qk[n][m] = f32x4{0.f, 0.f, 0.f, 0.f};
-    {
-      // the rows' fragments by depth chunk, two chunks in flight: chunk dd + 2
-      // is loaded into chunk dd's registers once its products are issued
-      // (half the operand registers of loading all four at once)
-      bf16x8 kf[2][4], qf[2][4];
-      auto load_dd = [&](int dd) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
-          qf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
-        }
-      };
-      load_dd(0);
-      load_dd(1);
-#pragma unroll
-      for (int dd = 0; dd < 4; ++dd) {
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-#pragma unroll
-          for (int n = 0; n <= m; ++n) {
-            kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
-            qk[n][m] = mfma16(kf[dd & 1][n], qf[dd & 1][m], qk[n][m]);
-          }
-        if (dd + 2 < 4) load_dd(dd + 2);
-      }
-    }
+    chunk_grams(q, k, t0, c, hq, lane, kk, qk);
 
     const int h0 = kGva * hq + e0;
     float alog[kGva], dtb[kGva];
@@ -1583,6 +1603,92 @@ __device__ __forceinline__ void full_head_items(
   };
   while (stage(std::integral_constant<int, 0>{}) && stage(std::integral_constant<int, 1>{})) {
   }
+}
+
+// ============================================================================
+// direct path: calls of at most one chunk in total (T <= 64)
+// ============================================================================
+// Every sequence then fits one chunk and the call is latency-bound, so it runs
+// as one launch with no plan and no workspace: one work-group per (sequence,
+// v-head).  All waves issue their share of the chunk's K / Q / V copies and
+// load their state tile; wave 0 then forms the chunk's terms (the prepass of
+// one item, written to LDS instead of the workspace) while those land, and
+// the eight waves run the chunk as the full-head consumer does.
+constexpr int kDirectMaxSeqs = 64;
+
+struct DirectSmem {
+  ConsumerSmem c;     // operands in buffer 0
+  PrepassWaveSmem w;  // wave 0's scratch for the terms
+};
+
+__global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const float* __restrict__ state, const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const float* __restrict__ dt_bias, const uint16_t* __restrict__ b, const void* __restrict__ cu, int is64,
+    long long T, float scale, uint16_t* __restrict__ out, float* __restrict__ new_state) {
+  __shared__ DirectSmem sm;
+  const int s = static_cast<int>(blockIdx.x) / kVHeads;
+  const int h = static_cast<int>(blockIdx.x) % kVHeads;
+  const int hq = h / kGva;
+  long long t0, t1;
+  seq_bounds(cu, is64, s, T, t0, t1);
+  const int c = static_cast<int>(t1 - t0);   // 0 .. T <= 64
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int vcol = 16 * w;
+  auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
+  const size_t soff = ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim + 8 * lg;
+  float* dst = new_state + soff;
+  if (c <= 0) {   // an empty sequence: zero state, no output rows
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+      __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f32x4*>(dst + kappa0(kt)));
+    return;
+  }
+  // the chunk's K / Q / V rows into buffer 0 (rows past c repeat row c - 1)
+  {
+    const int r = 4 * w + (lane >> 4);
+    const uint32_t kq_col = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(r));
+    const uint32_t v_col = 16u * static_cast<uint32_t>((lane & 15) ^ v_swz(r));
+    const size_t qk0 = (static_cast<size_t>(t0) * kQKHeads + hq) * kDim;
+    const char* kb = reinterpret_cast<const char*>(k + qk0);
+    const char* qb = reinterpret_cast<const char*>(q + qk0);
+    const char* vb = reinterpret_cast<const char*>(v + (static_cast<size_t>(t0) * kVHeads + h) * kDim);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t row = static_cast<uint32_t>(min(r + 32 * j, c - 1));
+      const uint32_t off = row * (kQKHeads * kDim * 2) + kq_col;
+      dma16(kb + off, &sm.c.ks[0][32 * j + 4 * w][0]);
+      dma16(qb + off, &sm.c.qs[0][32 * j + 4 * w][0]);
+      dma16<2>(vb + row * (kVHeads * kDim * 2) + v_col, &sm.c.vs[0][32 * j + 4 * w][0]);
+    }
+  }
+  f32x4 st[8];
+  if (state != nullptr) {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt)
+      st[kt] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(state + soff + kappa0(kt)));
+  } else {
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (w == 0) {
+    const size_t gi = static_cast<size_t>(t0 + min(lane, c - 1)) * kVHeads + h;
+    const float a1[kGva] = {bf2f(a[gi]), 0.0f}, b1[kGva] = {bf2f(b[gi]), 0.0f};
+    const float al1[kGva] = {A_log[h], 0.0f}, dt1[kGva] = {dt_bias[h], 0.0f};
+    f32x4 kk[4][4], qk[4][4];
+    chunk_grams(q, k, t0, c, hq, lane, kk, qk);
+    prepass_heads<1, true>(sm.w, kk, qk, c, a1, b1, al1, dt1, &sm.c.frag[0][0][0], &sm.c.gt[0][0]);
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // copies, state loads and the terms have landed
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
+      out + (static_cast<size_t>(t0) * kVHeads + h) * kDim, 0, c * (kVHeads * kDim * 2), 0x00020000);
+  consumer_chunk<0>(sm.c, c, st, w, lane, scale, orc, 2u * static_cast<uint32_t>(vcol + 4 * lg));
+#pragma unroll
+  for (int kt = 0; kt < 8; ++kt) __builtin_nontemporal_store(st[kt], reinterpret_cast<f32x4*>(dst + kappa0(kt)));
 }
 
 // ============================================================================
@@ -2509,6 +2615,15 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
   const auto* bb = static_cast<const uint16_t*>(b);
   auto* ob = static_cast<uint16_t*>(output);
   const int Ri = static_cast<int>(R), gc = static_cast<int>(gcap);
+
+  // at most one chunk in the whole call: one launch, no workspace traffic
+  if (total_tokens <= kChunk && num_seqs <= kDirectMaxSeqs) {
+    direct_kernel<<<dim3(static_cast<unsigned>(num_seqs * kVHeads)), dim3(kConsumerThreads), 0, st>>>(
+        qb, kb, vb, state, A_log, ab, dt_bias, bb, cu_seqlens, cu_seqlens_is_int64, total_tokens, scale, ob,
+        new_state);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? GDN_OK : static_cast<int>(e);
+  }
 
   // small batches: every prepass work-group finds its own record (one launch
   // fewer); large ones: a separate plan launch numbers the records once

@@ -42,6 +42,27 @@ def test_prefill_ragged(gpu, lengths):
            f"prefill ragged {lengths}")
 
 
+@pytest.mark.parametrize("lengths,zero_state,cu64", [
+    ([16], False, False), ([64], True, False), ([10, 0, 20, 34], False, True), ([1] * 64, False, False),
+    ([0, 0, 0, 5, 0], True, True), ([0, 0], False, False)])
+def test_prefill_direct(gpu, lengths, zero_state, cu64):
+    # at most 64 tokens and 64 sequences in the call: the single-launch direct
+    # path (terms formed in LDS by one wave, then the chunk), no workspace use
+    p = prefill_inputs_from_lengths(lengths, seed=len(lengths) * 7 + sum(lengths), zero_state=zero_state,
+                                    cu_dtype=torch.int64 if cu64 else torch.int32)
+    _check(p, gpu, f"prefill direct {lengths[:8]} zero_state={zero_state} int64={cu64}")
+
+
+def test_prefill_direct_state_none_and_boundary(gpu):
+    # state=None on the direct path, and just past its limits (65 sequences;
+    # 65 tokens) on the planned path, all against the oracle
+    p = prefill_inputs_from_lengths([7, 0, 40], seed=91)
+    p.state = None
+    _check(p, gpu, "prefill direct state=None")
+    _check(prefill_inputs_from_lengths([1] * 60 + [0] * 5, seed=92), gpu, "prefill 65 sequences, 60 tokens")
+    _check(prefill_inputs_from_lengths([30, 35], seed=93), gpu, "prefill 65 tokens in two sequences")
+
+
 @pytest.mark.parametrize("lengths", [[2048, 100], [1500, 0, 333, 1000, 64], [4096], [700, 3000, 65, 1300]])
 def test_prefill_segmented(gpu, lengths):
     # long sequences are cut into segments that run concurrently (zero-state
