@@ -138,13 +138,17 @@ constexpr int kListHdr = 16;
 constexpr int kRunM = 1;
 constexpr int kRunFromState = 2;
 
-// Finish work: a correction block is kFinChunks chunks of one (segment, v-head);
-// the four waves of a finish group split its chunks, then a chunk's 16-token tiles.
+// Finish work: a correction block is one or more chunks of one (segment,
+// v-head); wave w of a finish group corrects 16-token tile w of each chunk.
+// A block first forms the segment's starting state, which for segment j can
+// take up to j - 1 scan steps.  The M-run of a segment j >= kFinBlockSeg that
+// formed more than kFinBlockChunks chunks lists blocks of kFinBlockChunks
+// chunks, so that state is formed once per block rather than once per chunk;
+// otherwise it lists one block per chunk, and the blocks run in parallel.
 constexpr int kFinThreads = 256;
-constexpr int kFinChunks = 1;                             // chunks per correction block
-constexpr int kFinWpc = kFinThreads / 64 / kFinChunks;    // waves per chunk
-constexpr int kFinTpw = kChunk / 16 / kFinWpc;            // 16-token tiles per wave
-static_assert(kFinWpc * kFinChunks == kFinThreads / 64 && kFinTpw * kFinWpc == kChunk / 16, "finish tiling");
+constexpr int kFinBlockChunks = 4;
+constexpr int kFinBlockSeg = 3;
+static_assert(kFinThreads / 64 == kChunk / 16, "finish tiling: one wave per 16-token tile");
 __host__ __device__ inline long long max_runs(int num_seqs, long long gcap) { return 2 * gcap + num_seqs; }
 
 struct ListView {
@@ -2148,13 +2152,14 @@ __device__ __forceinline__ void split_items(
   };
   const SplitDmaLane dl = split_dma_lane(wt, lane, hv);
   // Correction blocks of the segment: chunks [0, formed) get O0 + OI S_j^T in
-  // the finish.  Each M-run (once per v-head) reserves a block per kFinChunks
-  // chunks with records during its first chunk (the atomic returns before
-  // that chunk's closing barrier, with the next chunk's copies), and fills
-  // them at its end, blocks past `formed` left empty.  The finish then takes
-  // one block per group with a single descriptor load.  The entry repeats the
-  // later-segment table's.
-  const int fix_max = (n + kFinChunks - 1) / kFinChunks;
+  // the finish.  Each M-run (once per v-head) reserves a block per chunk with
+  // records during its first chunk (the atomic returns before that chunk's
+  // closing barrier, with the next chunk's copies), and fills them at its end
+  // with blocks of one chunk, or of kFinBlockChunks chunks (see kFinBlockSeg);
+  // blocks past `formed` are left empty.  The finish then
+  // takes one block per group with a single descriptor load.  The entry
+  // repeats the later-segment table's.
+  const int fix_max = n;
   int fix_pos = 0;
 
   // An M-run stops once the bound of its map falls below kNegligibleLog2: its
@@ -2221,9 +2226,10 @@ __device__ __forceinline__ void split_items(
   if (mrun && tid == 0) mval[static_cast<size_t>(slot) * kVHeads + h] = formed | (formed < n ? kMNegligible : 0);
   if (mrun && hv == 0 && tid == kFixLane && fix_max > 0) {
     const int4 seg = make_int4(rb.x, rb.y, ((nrun - 1) * kChunk + last_tok) | (jseg << 17), slot - 1);
+    const int bsz = formed > kFinBlockChunks && jseg >= kFinBlockSeg ? kFinBlockChunks : 1;
     for (int b = 0; b < fix_max && fix_pos + b < fix_cap; ++b) {
       fix[2 * (fix_pos + b)] = seg;
-      fix[2 * (fix_pos + b) + 1] = make_int4(h, b * kFinChunks, min((b + 1) * kFinChunks, formed), 0);
+      fix[2 * (fix_pos + b) + 1] = make_int4(h, b * bsz, min((b + 1) * bsz, formed), 0);
     }
   }
 
@@ -2308,11 +2314,10 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 // B_j itself: the state before segment j is rebuilt from the latest such
 // segment before it (or from S_1), with scan steps only across segments whose
 // maps are not negligible.  Work items, one work-group each:
-//   a correction block (segment j >= 1, v-head, kFinChunks chunks whose OI was
-//        formed), as the consumer's M-run appended it: S_j, then out =
-//        bf16(O0 + OI S_j^T) for the block's chunks (the other chunks keep
-//        O0); the four waves split the block's chunks, and within a chunk its
-//        four 16-token tiles;
+//   a correction block (segment j >= 1, v-head, one or kFinBlockChunks chunks
+//        whose OI was formed), as the consumer's M-run appended it: S_j, then
+//        out = bf16(O0 + OI S_j^T) for the block's chunks (the other chunks
+//        keep O0), chunk by chunk, wave w taking 16-token tile w;
 //   (multi-segment sequence, v-head): new_state = S_nseg.
 // A scan step forms D = M^T S^T on MFMA with M^T as the M-run stored it (bf16
 // hi / lo) and S split into hi / lo from LDS (three products, fp32
@@ -2468,20 +2473,15 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
     const int first = static_cast<int>(fb.y);
     const int last = min(static_cast<int>(fb.z), (tok + kChunk - 1) / kChunk);
     if (first >= last) continue;
-    // wave w corrects token tiles [tt0, tt0 + kFinTpw) of chunk first + w / kFinWpc
-    // (all 128 value rows); its OI and O0 loads are issued before the state is formed
+    // wave w corrects token tile w of each chunk of the block (all 128 value
+    // rows); the first chunk's OI and O0 loads are issued before the state is
+    // formed, each later chunk's after the previous chunk's stores
     const long long c0s = static_cast<long long>(static_cast<unsigned>(sg.x)) | (static_cast<long long>(sg.y) << 32);
-    const int ci = first + w / kFinWpc;
-    const int tt0 = (w % kFinWpc) * kFinTpw;
-    const bool active = ci < last;
-    bf16x8 b[kFinTpw][4];   // [token tile][d]: OI rows as B fragments
-    u32x2 o0[kFinTpw][8];   // [token tile][value tile]: O0, four value columns
-    __amdgpu_buffer_rsrc_t orc = buf_rsrc(out, 0);
-    // the usual starting slot of the state rebuild, loaded with the outputs
-    const int prev = j >= 2 ? mval[static_cast<size_t>(g0 + j - 1) * kVHeads + h] : kMNegligible;
-    f32x4 slot0[kFinPer];
-    load_slot(slotb + (static_cast<size_t>(g0 + j - 1) * kVHeads + h) * kHeadState, slot0);
-    if (active) {
+    const uint32_t trow = static_cast<uint32_t>(16 * w + l16) * (kVHeads * kDim * 2);
+    bf16x8 b[4];   // [d]: OI rows as B fragments
+    u32x2 o0[8];   // [value tile]: O0, four value columns
+    __amdgpu_buffer_rsrc_t orc;
+    auto load_chunk = [&](int ci) {
       const long long c0 = c0s + static_cast<long long>(ci) * kChunk;
       const int c = min(kChunk, tok - ci * kChunk);
       const size_t rowbase = (static_cast<size_t>(c0) * kVHeads + h) * kDim;
@@ -2489,17 +2489,16 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
       orc = buf_rsrc(out + rowbase, bytes);
       const __amdgpu_buffer_rsrc_t irc = buf_rsrc(oi + rowbase, bytes);
 #pragma unroll
-      for (int tt = 0; tt < kFinTpw; ++tt) {
-        const uint32_t trow = static_cast<uint32_t>(16 * (tt0 + tt) + l16) * (kVHeads * kDim * 2);
+      for (int d = 0; d < 4; ++d)
+        b[d] = __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
-          b[tt][d] = __builtin_bit_cast(
-              bf16x8, __builtin_amdgcn_raw_buffer_load_b128(irc, trow + 2 * (32 * d + 8 * lg), 0, 0));
-#pragma unroll
-        for (int vt = 0; vt < 8; ++vt)
-          o0[tt][vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
-      }
-    }
+      for (int vt = 0; vt < 8; ++vt) o0[vt] = __builtin_amdgcn_raw_buffer_load_b64(orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
+    };
+    // the usual starting slot of the state rebuild, loaded with the outputs
+    const int prev = j >= 2 ? mval[static_cast<size_t>(g0 + j - 1) * kVHeads + h] : kMNegligible;
+    f32x4 slot0[kFinPer];
+    load_slot(slotb + (static_cast<size_t>(g0 + j - 1) * kVHeads + h) * kHeadState, slot0);
+    load_chunk(first);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();   // the previous item's readers of sm are done
     state_before(sm, g0, j, h, slotb, slotm, mval, w, lane, slot0, prev);
@@ -2521,27 +2520,17 @@ __global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ l
 #pragma unroll
       for (int d = 0; d < 4; ++d) sm.frag[2 * w + e][d][lane] = fr[e][d];
     __syncthreads();
-    if (active) {
+    for (int ci = first; ci < last; ++ci) {
+      if (ci > first) load_chunk(ci);
 #pragma unroll
       for (int vt = 0; vt < 8; ++vt) {
-        // independent accumulators (token tiles)
-        f32x4 acc[kFinTpw];
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int tt = 0; tt < kFinTpw; ++tt) acc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          const bf16x8 a_ = __builtin_bit_cast(bf16x8, sm.frag[vt][d][lane]);
-#pragma unroll
-          for (int tt = 0; tt < kFinTpw; ++tt) acc[tt] = mfma16(a_, b[tt][d], acc[tt]);
-        }
-#pragma unroll
-        for (int tt = 0; tt < kFinTpw; ++tt) {
-          const u32x2 o = o0[tt][vt];
-          const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[tt][0], bf_hi(o.x) + acc[tt][1]),
-                            pack_bf2(bf_lo(o.y) + acc[tt][2], bf_hi(o.y) + acc[tt][3])};
-          const uint32_t trow = static_cast<uint32_t>(16 * (tt0 + tt) + l16) * (kVHeads * kDim * 2);
-          __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
-        }
+        for (int d = 0; d < 4; ++d) acc = mfma16(__builtin_bit_cast(bf16x8, sm.frag[vt][d][lane]), b[d], acc);
+        const u32x2 o = o0[vt];
+        const u32x2 o1 = {pack_bf2(bf_lo(o.x) + acc[0], bf_hi(o.x) + acc[1]),
+                          pack_bf2(bf_lo(o.y) + acc[2], bf_hi(o.y) + acc[3])};
+        __builtin_amdgcn_raw_buffer_store_b64(o1, orc, trow + 2 * (16 * vt + 4 * lg), 0, 0);
       }
     }
   }
