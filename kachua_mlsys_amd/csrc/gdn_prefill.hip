@@ -64,9 +64,9 @@ constexpr int kBoundAt = 2 * kChunk;
 // g_t (I - beta_t k_t k_t^T), whose 2-norm is at most g_t max(1, |1 - beta_t |k_t|^2|).
 // The prepass stores the chunk's sum of log2 of these factors; once a run from
 // the identity (an M-run) has accumulated less than kNegligibleLog2, its state
-// and all later outputs are below 2^-60 of the state they multiply and the run
-// stops.
-constexpr float kNegligibleLog2 = -60.0f;
+// and all later outputs are below 2^-30 (1e-9) of the state they multiply, far
+// below the fp32 rounding of the results they are added to, and the run stops.
+constexpr float kNegligibleLog2 = -30.0f;
 // Chunks whose map bound is above this (log2) carry the state into X = K S^T
 // as a bf16 hi + lo pair instead of one bf16 (see chain_chunk).
 constexpr float kHiLoBoundLog2 = -8.0f;
@@ -2310,7 +2310,7 @@ void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict_
 // finish: states before segments, output correction, final states
 // ============================================================================
 // S_{j+1} = S_j M_j + B_j and O_j = O0_j + OI_j S_j^T.  An M-run that stopped
-// early (kMNegligible) has a map below 2^-60, so the state after its segment is
+// early (kMNegligible) has a map below 2^-30, so the state after its segment is
 // B_j itself: the state before segment j is rebuilt from the latest such
 // segment before it (or from S_1), with scan steps only across segments whose
 // maps are not negligible.  Work items, one work-group each:
