@@ -836,8 +836,11 @@ __device__ __forceinline__ void store_frag(const u32x4& x, uint16_t* dst) {
 // k_t . k_i; qk[a][m] (a <= m) holds [i = 16 a + 4 lg + rr][t = 16 m + l16] =
 // k_i . q_t.  a_t, b_t: this lane's token (clamped into the chunk) per v-head.
 // The terms go to frag0 / gp0 in the workspace layout: global memory
-// (streamed out), or LDS when kToLds (the direct path).
-template <int NH, bool kToLds = false>
+// (streamed out), or LDS when kToLds (the direct path).  NB: the number of
+// 16-token blocks that hold tokens (c <= 16 NB).  Later blocks have beta = 0,
+// so their rows of N, their columns of Aqk and every fragment of Tb that
+// touches them are exactly zero: they are stored as zeros without being formed.
+template <int NH, bool kToLds = false, int NB = 4>
 __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4], const f32x4 (&qk)[4][4],
                                               int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
                                               const float (&alog)[kGva], const float (&dtb)[kGva],
@@ -892,7 +895,8 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const int i = 16 * ai + 4 * lg + rr, t = 16 * m + l16;
-            x[4 * hf + rr] = (ai <= m && i <= t) ? fast_exp2(lcol[e][m] - lrow[e][ai][rr]) * qk[ai][m][rr] : 0.0f;
+            x[4 * hf + rr] = (ai <= m && m < NB && i <= t)
+                                 ? fast_exp2(lcol[e][m] - lrow[e][ai][rr]) * qk[ai][m][rr] : 0.0f;
           }
         }
         store_frag<kToLds>(
@@ -918,14 +922,14 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int t = 16 * m + 4 * lg + rr, i = 16 * n + l16;
-          nv[rr] = i < t ? brow[e][m][rr] * fast_exp2(lrow[e][m][rr] - lcol[e][n]) * kk[m][n][rr] : 0.0f;
+          nv[rr] = (m < NB && i < t) ? brow[e][m][rr] * fast_exp2(lrow[e][m][rr] - lcol[e][n]) * kk[m][n][rr] : 0.0f;
         }
         if (n == m) {
           // t = 16 m + l16 sits on the lane whose rows include it (rr = l16 - 4 lg);
           // rows t >= c have beta = 0 and contribute 0
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr)
-            if (l16 == 4 * lg + rr) kb[e] += __log2f(fmaxf(1.0f, fabsf(1.0f - brow[e][m][rr] * kk[m][m][rr])));
+            if (m < NB && l16 == 4 * lg + rr) kb[e] += __log2f(fmaxf(1.0f, fabsf(1.0f - brow[e][m][rr] * kk[m][m][rr])));
           *reinterpret_cast<f32x4*>(&ws.nt[e][m][l16][4 * lg]) = nv;
         } else {
           nlo[e][m][n] = nv;
@@ -1000,9 +1004,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
       for (int a = 0; a < m; ++a) nx[m][a] = split_x(nlo[e][m][a]);
     }
 #pragma unroll
-    for (int dist = 1; dist < 4; ++dist) {
+    for (int dist = 1; dist < NB; ++dist) {
 #pragma unroll
-      for (int ab = 0; ab + dist < 4; ++ab) {
+      for (int ab = 0; ab + dist < NB; ++ab) {
         const int bb = ab + dist;
         // P = sum_m U_am W_mb, the term of the block formed last (m = ab + 1)
         // added last, so only it waits for the previous distance
@@ -1023,7 +1027,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
         for (int hf = 0; hf < 2; ++hf) {
           const int ai = 2 * d + hf;
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = ai <= m ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
+          for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = (ai <= m && m < NB) ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
         }
         store_frag<kToLds>(
             u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])},
@@ -1046,30 +1050,32 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 // Fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
 // columns 32 d + 8 lg .. + 7.  Rows past the chunk end repeat row c - 1: they
 // meet beta = 0 (rows of N), i <= t masks and output rows never stored.
+// Only the tiles of the first NB 16-row blocks are formed.
+template <int NB = 4>
 __device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                             long long t0, int c, int hq, int lane, f32x4 (&kk)[4][4],
                                             f32x4 (&qk)[4][4]) {
   const int l16 = lane & 15, lg = lane >> 4;
   const int cm1 = c - 1;
-  const uint16_t* krow[4];
-  const uint16_t* qrow[4];
+  const uint16_t* krow[NB];
+  const uint16_t* qrow[NB];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < NB; ++m) {
     const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
     krow[m] = k + (row * kQKHeads + hq) * kDim + 8 * lg;
     qrow[m] = q + (row * kQKHeads + hq) * kDim + 8 * lg;
   }
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < NB; ++m)
 #pragma unroll
     for (int n = 0; n <= m; ++n) kk[m][n] = qk[n][m] = f32x4{0.f, 0.f, 0.f, 0.f};
   // the rows' fragments by depth chunk, two chunks in flight: chunk dd + 2 is
   // loaded into chunk dd's registers once its products are issued (half the
   // operand registers of loading all four at once)
-  bf16x8 kf[2][4], qf[2][4];
+  bf16x8 kf[2][NB], qf[2][NB];
   auto load_dd = [&](int dd) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < NB; ++m) {
       kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
       qf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
     }
@@ -1079,7 +1085,7 @@ __device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ q, cons
 #pragma unroll
   for (int dd = 0; dd < 4; ++dd) {
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < NB; ++m)
 #pragma unroll
       for (int n = 0; n <= m; ++n) {
         kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
@@ -1682,9 +1688,19 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
     const size_t gi = static_cast<size_t>(t0 + min(lane, c - 1)) * kVHeads + h;
     const float a1[kGva] = {bf2f(a[gi]), 0.0f}, b1[kGva] = {bf2f(b[gi]), 0.0f};
     const float al1[kGva] = {A_log[h], 0.0f}, dt1[kGva] = {dt_bias[h], 0.0f};
-    f32x4 kk[4][4], qk[4][4];
-    chunk_grams(q, k, t0, c, hq, lane, kk, qk);
-    prepass_heads<1, true>(sm.w, kk, qk, c, a1, b1, al1, dt1, &sm.c.frag[0][0][0], &sm.c.gt[0][0]);
+    // only the 16-token blocks that hold tokens are formed (c <= 16 nb)
+    auto terms = [&](auto NBC) {
+      constexpr int NB = decltype(NBC)::value;
+      f32x4 kk[4][4], qk[4][4];
+      chunk_grams<NB>(q, k, t0, c, hq, lane, kk, qk);
+      prepass_heads<1, true, NB>(sm.w, kk, qk, c, a1, b1, al1, dt1, &sm.c.frag[0][0][0], &sm.c.gt[0][0]);
+    };
+    switch ((c + 15) >> 4) {
+      case 1: terms(std::integral_constant<int, 1>{}); break;
+      case 2: terms(std::integral_constant<int, 2>{}); break;
+      case 3: terms(std::integral_constant<int, 3>{}); break;
+      default: terms(std::integral_constant<int, 4>{}); break;
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);   // copies, state loads and the terms have landed
   __syncthreads();
