@@ -267,24 +267,25 @@ def time_prefill(p_cpu, args, torch, dev, traffic=None, warm=None) -> dict:
 
 
 def chain_step_us(args, torch, dev) -> dict:
-    """Time of one chunk step of the sequential state chain: one sequence of
-    4 chunks against one of 2 (warm cache; too short to be cut into segments,
-    so the difference is two chunk steps of the consumer's chain)."""
+    """Time of one chunk step of the consumer's sequential state chain: one
+    sequence of 4 chunks against one of 3 (warm cache; both too short to be
+    cut into segments and too long for the direct path, so the difference is
+    one chunk step of the chain)."""
     from kachua_mlsys_amd.inputs import prefill_inputs_from_lengths
 
     t = {}
-    for nch in (2, 4):
+    for nch in (3, 4):
         p = prefill_inputs_from_lengths([64 * nch], seed=11)
         t[nch] = time_prefill(p, args, torch, dev, warm=True)["us_per_call"]
-    return {"us": round((t[4] - t[2]) / 2, 3), "us_per_call_2_chunks": t[2], "us_per_call_4_chunks": t[4],
-            "method": "(t(1 x 256 tokens) - t(1 x 128 tokens)) / 2, warm cache"}
+    return {"us": round(t[4] - t[3], 3), "us_per_call_3_chunks": t[3], "us_per_call_4_chunks": t[4],
+            "method": "t(1 x 256 tokens) - t(1 x 192 tokens), warm cache"}
 
 
 # Prefill workloads beside the three configurations: configuration 3 with
 # near-1 decay (every chunk takes the state's bf16 lo pass, and the segment
-# maps stay large), and one-sequence prompts shorter than a chunk and of one
-# chunk, where a call is launch-bound.
-EXTRA_PREFILL = ("c3_slow_decay", "t16", "t64")
+# maps stay large), and one-sequence prompts of 16, 64 and 128 tokens, where a
+# call is launch-bound (the direct path).
+EXTRA_PREFILL = ("c3_slow_decay", "t16", "t64", "t128")
 
 
 def extra_prefill_inputs(name):
@@ -300,6 +301,8 @@ def extra_prefill_inputs(name):
         return prefill_inputs_from_lengths([16], seed=16)
     if name == "t64":
         return prefill_inputs_from_lengths([64], seed=64)
+    if name == "t128":
+        return prefill_inputs_from_lengths([128], seed=128)
     raise ValueError(f"unknown extra prefill workload {name!r} (known: {', '.join(EXTRA_PREFILL)})")
 
 

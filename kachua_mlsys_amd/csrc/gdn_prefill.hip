@@ -1616,19 +1616,21 @@ __device__ __forceinline__ void full_head_items(
 }
 
 // ============================================================================
-// direct path: calls of at most one chunk in total (T <= 64)
+// direct path: calls of at most two chunks in total (T <= 128)
 // ============================================================================
-// Every sequence then fits one chunk and the call is latency-bound, so it runs
-// as one launch with no plan and no workspace: one work-group per (sequence,
-// v-head).  All waves issue their share of the chunk's K / Q / V copies and
-// load their state tile; wave 0 then forms the chunk's terms (the prepass of
-// one item, written to LDS instead of the workspace) while those land, and
-// the eight waves run the chunk as the full-head consumer does.
+// Every sequence then has at most two chunks and the call is latency-bound, so
+// it runs as one launch with no plan and no workspace: one work-group per
+// (sequence, v-head).  All waves issue their share of the chunks' K / Q / V
+// copies (chunk j into buffer j) and load their state tile; wave j then forms
+// chunk j's terms (the prepass of one item, written to LDS instead of the
+// workspace) while those land, and the eight waves run the chunks one after
+// the other as the full-head consumer does, the state staying in registers.
 constexpr int kDirectMaxSeqs = 64;
+constexpr int kDirectMaxChunks = 2;
 
 struct DirectSmem {
-  ConsumerSmem c;     // operands in buffer 0
-  PrepassWaveSmem w;  // wave 0's scratch for the terms
+  ConsumerSmem c;                         // chunk j's operands in buffer j
+  PrepassWaveSmem w[kDirectMaxChunks];    // scratch of the terms waves
 };
 
 __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
@@ -1642,7 +1644,8 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
   const int hq = h / kGva;
   long long t0, t1;
   seq_bounds(cu, is64, s, T, t0, t1);
-  const int c = static_cast<int>(t1 - t0);   // 0 .. T <= 64
+  const int len = static_cast<int>(t1 - t0);   // 0 .. T <= 128
+  const int nch = (len + kChunk - 1) / kChunk;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -1651,30 +1654,36 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
   auto kappa0 = [](int kt) { return 32 * (kt >> 1) + 4 * (kt & 1); };
   const size_t soff = ((static_cast<size_t>(s) * kVHeads + h) * kDim + vcol + l16) * kDim + 8 * lg;
   float* dst = new_state + soff;
-  if (c <= 0) {   // an empty sequence: zero state, no output rows
+  if (len <= 0) {   // an empty sequence: zero state, no output rows
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt)
       __builtin_nontemporal_store(f32x4{0.f, 0.f, 0.f, 0.f}, reinterpret_cast<f32x4*>(dst + kappa0(kt)));
     return;
   }
-  // the chunk's K / Q / V rows into buffer 0 (rows past c repeat row c - 1)
-  {
+  // chunk j: first token t0 + 64 j, c_j tokens
+  auto chunk_len = [&](int j) { return min(kChunk, len - kChunk * j); };
+  // chunk j's K / Q / V rows into buffer j (rows past c_j repeat its last row)
+  auto copy = [&](auto JC) {
+    constexpr int J = decltype(JC)::value;
     const int r = 4 * w + (lane >> 4);
     const uint32_t kq_col = 16u * static_cast<uint32_t>((lane & 15) ^ kq_swz(r));
     const uint32_t v_col = 16u * static_cast<uint32_t>((lane & 15) ^ v_swz(r));
-    const size_t qk0 = (static_cast<size_t>(t0) * kQKHeads + hq) * kDim;
+    const long long c0 = t0 + static_cast<long long>(kChunk) * J;
+    const size_t qk0 = (static_cast<size_t>(c0) * kQKHeads + hq) * kDim;
     const char* kb = reinterpret_cast<const char*>(k + qk0);
     const char* qb = reinterpret_cast<const char*>(q + qk0);
-    const char* vb = reinterpret_cast<const char*>(v + (static_cast<size_t>(t0) * kVHeads + h) * kDim);
+    const char* vb = reinterpret_cast<const char*>(v + (static_cast<size_t>(c0) * kVHeads + h) * kDim);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t row = static_cast<uint32_t>(min(r + 32 * j, c - 1));
+    for (int jj = 0; jj < 2; ++jj) {
+      const uint32_t row = static_cast<uint32_t>(min(r + 32 * jj, chunk_len(J) - 1));
       const uint32_t off = row * (kQKHeads * kDim * 2) + kq_col;
-      dma16(kb + off, &sm.c.ks[0][32 * j + 4 * w][0]);
-      dma16(qb + off, &sm.c.qs[0][32 * j + 4 * w][0]);
-      dma16<2>(vb + row * (kVHeads * kDim * 2) + v_col, &sm.c.vs[0][32 * j + 4 * w][0]);
+      dma16(kb + off, &sm.c.ks[J][32 * jj + 4 * w][0]);
+      dma16(qb + off, &sm.c.qs[J][32 * jj + 4 * w][0]);
+      dma16<2>(vb + row * (kVHeads * kDim * 2) + v_col, &sm.c.vs[J][32 * jj + 4 * w][0]);
     }
-  }
+  };
+  copy(std::integral_constant<int, 0>{});
+  if (nch > 1) copy(std::integral_constant<int, 1>{});
   f32x4 st[8];
   if (state != nullptr) {
 #pragma unroll
@@ -1684,29 +1693,40 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) st[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  if (w == 0) {
-    const size_t gi = static_cast<size_t>(t0 + min(lane, c - 1)) * kVHeads + h;
+  // wave j < nch forms chunk j's terms into buffer j
+  auto terms = [&](auto JC) {
+    constexpr int J = decltype(JC)::value;
+    const int c = chunk_len(J);
+    const long long c0 = t0 + static_cast<long long>(kChunk) * J;
+    const size_t gi = static_cast<size_t>(c0 + min(lane, c - 1)) * kVHeads + h;
     const float a1[kGva] = {bf2f(a[gi]), 0.0f}, b1[kGva] = {bf2f(b[gi]), 0.0f};
     const float al1[kGva] = {A_log[h], 0.0f}, dt1[kGva] = {dt_bias[h], 0.0f};
     // only the 16-token blocks that hold tokens are formed (c <= 16 nb)
-    auto terms = [&](auto NBC) {
+    auto blocks = [&](auto NBC) {
       constexpr int NB = decltype(NBC)::value;
       f32x4 kk[4][4], qk[4][4];
-      chunk_grams<NB>(q, k, t0, c, hq, lane, kk, qk);
-      prepass_heads<1, true, NB>(sm.w, kk, qk, c, a1, b1, al1, dt1, &sm.c.frag[0][0][0], &sm.c.gt[0][0]);
+      chunk_grams<NB>(q, k, c0, c, hq, lane, kk, qk);
+      prepass_heads<1, true, NB>(sm.w[J], kk, qk, c, a1, b1, al1, dt1, &sm.c.frag[J][0][0], &sm.c.gt[J][0]);
     };
     switch ((c + 15) >> 4) {
-      case 1: terms(std::integral_constant<int, 1>{}); break;
-      case 2: terms(std::integral_constant<int, 2>{}); break;
-      case 3: terms(std::integral_constant<int, 3>{}); break;
-      default: terms(std::integral_constant<int, 4>{}); break;
+      case 1: blocks(std::integral_constant<int, 1>{}); break;
+      case 2: blocks(std::integral_constant<int, 2>{}); break;
+      case 3: blocks(std::integral_constant<int, 3>{}); break;
+      default: blocks(std::integral_constant<int, 4>{}); break;
     }
-  }
+  };
+  if (w == 0) terms(std::integral_constant<int, 0>{});
+  if (w == 1 && nch > 1) terms(std::integral_constant<int, 1>{});
   __builtin_amdgcn_s_waitcnt(0);   // copies, state loads and the terms have landed
   __syncthreads();
-  const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
-      out + (static_cast<size_t>(t0) * kVHeads + h) * kDim, 0, c * (kVHeads * kDim * 2), 0x00020000);
-  consumer_chunk<0>(sm.c, c, st, w, lane, scale, orc, 2u * static_cast<uint32_t>(vcol + 4 * lg));
+  const uint32_t ocol = 2u * static_cast<uint32_t>(vcol + 4 * lg);
+  auto out_rsrc = [&](int j) {
+    return __builtin_amdgcn_make_buffer_rsrc(out + ((static_cast<size_t>(t0) + kChunk * j) * kVHeads + h) * kDim, 0,
+                                             chunk_len(j) * (kVHeads * kDim * 2), 0x00020000);
+  };
+  // each wave carries its own state tile: no barrier between the chunks
+  consumer_chunk<0>(sm.c, chunk_len(0), st, w, lane, scale, out_rsrc(0), ocol);
+  if (nch > 1) consumer_chunk<1>(sm.c, chunk_len(1), st, w, lane, scale, out_rsrc(1), ocol);
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt) __builtin_nontemporal_store(st[kt], reinterpret_cast<f32x4*>(dst + kappa0(kt)));
 }
@@ -2621,8 +2641,8 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
   auto* ob = static_cast<uint16_t*>(output);
   const int Ri = static_cast<int>(R), gc = static_cast<int>(gcap);
 
-  // at most one chunk in the whole call: one launch, no workspace traffic
-  if (total_tokens <= kChunk && num_seqs <= kDirectMaxSeqs) {
+  // at most two chunks in the whole call: one launch, no workspace traffic
+  if (total_tokens <= static_cast<long long>(kDirectMaxChunks) * kChunk && num_seqs <= kDirectMaxSeqs) {
     direct_kernel<<<dim3(static_cast<unsigned>(num_seqs * kVHeads)), dim3(kConsumerThreads), 0, st>>>(
         qb, kb, vb, state, A_log, ab, dt_bias, bb, cu_seqlens, cu_seqlens_is_int64, total_tokens, scale, ob,
         new_state);

@@ -44,10 +44,12 @@ def test_prefill_ragged(gpu, lengths):
 
 @pytest.mark.parametrize("lengths,zero_state,cu64", [
     ([16], False, False), ([64], True, False), ([10, 0, 20, 34], False, True), ([1] * 64, False, False),
-    ([0, 0, 0, 5, 0], True, True), ([0, 0], False, False)])
+    ([0, 0, 0, 5, 0], True, True), ([0, 0], False, False), ([128], False, False), ([100, 28], False, True),
+    ([65, 0, 63], True, False), ([17, 111], False, False)])
 def test_prefill_direct(gpu, lengths, zero_state, cu64):
-    # at most 64 tokens and 64 sequences in the call: the single-launch direct
-    # path (terms formed in LDS by one wave, then the chunk), no workspace use
+    # at most 128 tokens and 64 sequences in the call: the single-launch
+    # direct path (each chunk's terms formed in LDS by one wave, then the
+    # chunks), no workspace use
     p = prefill_inputs_from_lengths(lengths, seed=len(lengths) * 7 + sum(lengths), zero_state=zero_state,
                                     cu_dtype=torch.int64 if cu64 else torch.int32)
     _check(p, gpu, f"prefill direct {lengths[:8]} zero_state={zero_state} int64={cu64}")
@@ -55,12 +57,13 @@ def test_prefill_direct(gpu, lengths, zero_state, cu64):
 
 def test_prefill_direct_state_none_and_boundary(gpu):
     # state=None on the direct path, and just past its limits (65 sequences;
-    # 65 tokens) on the planned path, all against the oracle
-    p = prefill_inputs_from_lengths([7, 0, 40], seed=91)
-    p.state = None
-    _check(p, gpu, "prefill direct state=None")
+    # 129 tokens) on the planned path, all against the oracle
+    for lengths in ([7, 0, 40], [90, 20]):
+        p = prefill_inputs_from_lengths(lengths, seed=91)
+        p.state = None
+        _check(p, gpu, f"prefill direct {lengths} state=None")
     _check(prefill_inputs_from_lengths([1] * 60 + [0] * 5, seed=92), gpu, "prefill 65 sequences, 60 tokens")
-    _check(prefill_inputs_from_lengths([30, 35], seed=93), gpu, "prefill 65 tokens in two sequences")
+    _check(prefill_inputs_from_lengths([64, 65], seed=93), gpu, "prefill 129 tokens in two sequences")
 
 
 @pytest.mark.parametrize("lengths", [[2048, 100], [1500, 0, 333, 1000, 64], [4096], [700, 3000, 65, 1300]])
