@@ -1124,17 +1124,45 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
   if (fused_plan) {
     const int nblk = (num_seqs + 63) / 64;
     if (wv == 0) {
+      // every block's bounds are requested before the first is scanned (one
+      // memory round trip instead of one per block)
+      // (lanes past the last sequence read a valid entry, then count as empty)
+      long long b0[kFusedBlocks], b1[kFusedBlocks];
+      if (is64) {
+        const long long* c64 = static_cast<const long long*>(cu);
+#pragma unroll
+        for (int j = 0; j < kFusedBlocks; ++j) {
+          const int i = min(64 * j + lane, num_seqs - 1);
+          b0[j] = c64[i];
+          b1[j] = c64[i + 1];
+        }
+      } else {
+        const int* c32 = static_cast<const int*>(cu);
+#pragma unroll
+        for (int j = 0; j < kFusedBlocks; ++j) {
+          const int i = min(64 * j + lane, num_seqs - 1);
+          b0[j] = c32[i];
+          b1[j] = c32[i + 1];
+        }
+      }
       int carry = 0;
-      for (int j = 0; j < nblk; ++j) {
-        const int s = 64 * j + lane;
-        long long t0 = 0, t1 = 0;
-        if (s < num_seqs) seq_bounds(cu, is64, s, T, t0, t1);
-        const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
-        const int inc = wave_incl_sum(nch) + carry;
-        sm.seq.incl[s] = inc;
-        sm.seq.s0[s] = t0;
-        sm.seq.s1[s] = t1;
-        carry = __builtin_amdgcn_readlane(inc, 63);
+#pragma unroll
+      for (int j = 0; j < kFusedBlocks; ++j) {
+        if (j < nblk) {
+          const int s = 64 * j + lane;
+          // the clamps of seq_bounds
+          long long t0 = b0[j] < 0 ? 0 : (b0[j] > T ? T : b0[j]);
+          long long t1 = b1[j] < t0 ? t0 : (b1[j] > T ? T : b1[j]);
+          if (s >= num_seqs) t0 = t1 = 0;
+          b0[j] = t0;
+          b1[j] = t1;
+          const int nch = static_cast<int>((b1[j] - b0[j] + kChunk - 1) / kChunk);
+          const int inc = wave_incl_sum(nch) + carry;
+          sm.seq.incl[s] = inc;
+          sm.seq.s0[s] = b0[j];
+          sm.seq.s1[s] = b1[j];
+          carry = __builtin_amdgcn_readlane(inc, 63);
+        }
       }
     }
     __syncthreads();
