@@ -78,9 +78,10 @@ def read_traffic(name: str):
     return float(m.group(1)) if m else None
 
 
-def time_launches(fn, sets, steps, warmup, torch):
+def time_launches(fn, sets, steps, warmup, torch, replays=1):
     """W eager warmup launches, then exactly `steps` launches (rotating over
-    `sets`) captured in one HIP graph and replayed once inside the timed region.
+    `sets`) captured in one HIP graph and replayed once inside the timed region
+    (`replays` > 1: that many timed replays, the median of their times).
 
     Returns (ms per step from HIP events on the launch stream around the replay,
     host wall ms per step for eager launches of the same work).  The graph keeps
@@ -102,15 +103,17 @@ def time_launches(fn, sets, steps, warmup, torch):
     graph.replay()                      # untimed: first replay uploads the graph
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record(stream)
-    graph.replay()
-    end.record(stream)
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    times = []
+    for _ in range(replays):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
     del graph
-    return ms, eager_ms
+    return sorted(times)[len(times) // 2], eager_ms
 
 
 def hbm_copy_gbps(torch, dev, nbytes=1 << 30, reps=10):
@@ -238,7 +241,9 @@ def time_prefill(p_cpu, args, torch, dev, traffic=None, warm=None) -> dict:
                            p.cu_seqlens, p.scale, s[3], s[4], workspace=s[5])
 
     steps = max(10, args.steps // 4)
-    ev_ms, wall_ms = time_launches(pre_step, sets, steps, max(3, args.warmup // 4), torch)
+    # secondary figures: the median of three timed replays, so that one
+    # disturbed replay does not set the number
+    ev_ms, wall_ms = time_launches(pre_step, sets, steps, max(3, args.warmup // 4), torch, replays=3)
     nbytes = prefill_bytes(T, N)
     flops = prefill_flops(p.lengths)
     t_s = ev_ms * 1e-3

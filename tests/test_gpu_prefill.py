@@ -116,6 +116,18 @@ def test_prefill_many_sequences(gpu, case):
     _check(prefill_inputs_from_lengths(lengths, seed=len(lengths)), gpu, f"prefill {case}")
 
 
+@pytest.mark.parametrize("n,cu64", [(512, True), (449, False), (65, True)])
+def test_prefill_fused_plan_blocks(gpu, n, cu64):
+    # up to 512 sequences: the prepass scans the sequence bounds itself, in
+    # blocks of 64 (all eight, a partial last block, two); short, empty and
+    # segmented sequences in one batch
+    g = torch.Generator().manual_seed(n)
+    lengths = [int(x) for x in torch.randint(0, 40, (n,), generator=g)]
+    lengths[3], lengths[n // 2], lengths[n - 1] = 700, 0, 300
+    p = prefill_inputs_from_lengths(lengths, seed=n + 1, cu_dtype=torch.int64 if cu64 else torch.int32)
+    _check(p, gpu, f"prefill {n} sequences (prepass scan) int64={cu64}")
+
+
 def test_prefill_segmented_state_none(gpu):
     p = prefill_inputs_from_lengths([1800, 900], seed=21)
     p.state = None
