@@ -103,3 +103,19 @@ def test_entry_points():
     assert contest.entry_point(contest.PREFILL) is prefill.launch_gdn
     with pytest.raises(KeyError):
         contest.entry_point("gdn_other")
+
+
+def test_contest_check_tolerance_rule():
+    # the reference harness's per-output rule: allclose(atol=rtol=1e-2), max abs
+    # and max rel (denominator clamped at 1e-12)
+    import contest_check
+
+    ref = torch.tensor([1.0, 2.0, 0.0])
+    e = contest_check._errors(ref, torch.tensor([1.005, 2.0, 0.0]))
+    assert e["within_tolerance"] and abs(e["max_abs_error"] - 0.005) < 1e-6 and abs(e["max_rel_error"] - 0.005) < 1e-5
+    e = contest_check._errors(ref, torch.tensor([1.05, 2.0, 0.0]))
+    assert not e["within_tolerance"] and abs(e["max_abs_error"] - 0.05) < 1e-6
+    e = contest_check._errors(ref, torch.tensor([1.0, 2.0, 0.005]))   # |x| <= atol near zero: within
+    assert e["within_tolerance"] and e["max_rel_error"] > 1e6
+    e = contest_check._errors(torch.empty(0), torch.empty(0))
+    assert e["within_tolerance"]
