@@ -105,7 +105,6 @@ constexpr int kMatElems = kMatFrags * kFragTile;   // one packed 64x64 matrix
 //   S_{j+1} = S_j M_j + B_j,          O_j = O0_j + OI_j S_j^T,
 // which a short scan over segments and a parallel correction pass resolve.
 constexpr int kMinSegChunks = 4;   // shortest segment the planner may choose
-constexpr int kMaxSegChunks = 1024;   // longest finite candidate (segments of multi-segment sequences)
 constexpr int kMSlotElems = 8 * 4 * 2 * 64 * 8;   // M_j^T as bf16 hi / lo MFMA fragments, per head
 
 // Upper bound on the segments of all multi-segment sequences: a sequence of
@@ -1112,7 +1111,6 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
     return;
   }
   const int lane = threadIdx.x & 63;
-  const int l16 = lane & 15, lg = lane >> 4;
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   PrepassWaveSmem& ws = sm.u.w[wv];
   const int gw = (static_cast<int>(blockIdx.x) - fused_plan) * kPrepassWaves + wv;
@@ -2349,8 +2347,7 @@ union ConsumerLds {
 __global__ __launch_bounds__(kSplitThreads)
 void consumer_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                      const uint16_t* __restrict__ v, const float* __restrict__ state,
-                     const void* __restrict__ cu, int is64, long long T, int R, int gcap, float scale,
-                     const int* __restrict__ rec_start, int* __restrict__ lists, int num_seqs,
+                     int R, int gcap, float scale, int* __restrict__ lists, int num_seqs,
                      int g_long, const uint16_t* __restrict__ ws_frag, const float* __restrict__ ws_gam,
                      uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
                      float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval,
@@ -2705,8 +2702,8 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
       total_tokens > kChunk ? std::min<long long>(max_runs(num_seqs, gcap) * 2 * kVHeads, kConsumerGroups) : 0;
   const long long g_short = std::min<long long>(static_cast<long long>(num_seqs) * kVHeads, kConsumerGroups);
   consumer_kernel<<<dim3(static_cast<unsigned>(g_long + g_short)), dim3(kSplitThreads), 0, st>>>(
-      qb, kb, vb, state, cu_seqlens, cu_seqlens_is_int64, total_tokens, Ri, gc, scale, rec_start, lists,
-      num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi, slotb, slotm, mval, fix);
+      qb, kb, vb, state, Ri, gc, scale, lists, num_seqs, static_cast<int>(g_long), frag, gam, ob, new_state, oi,
+      slotb, slotm, mval, fix);
   // a second segment needs more than kMinSegChunks chunks in one sequence and a slot
   if (gcap > 0 && total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
     const long long g_fin = std::min<long long>(R * kVHeads, 1024);
