@@ -63,7 +63,7 @@ int gdn_decode_fwd(const void* q, const void* k, const void* v, const float* sta
  * and `total_tokens` tokens (the caller allocates it; its contents on entry are
  * irrelevant).  The reference allocates the same kind of scratch per call with
  * torch.empty (gdn_prefill_qk4_v8_d128_k_last/solution/triton/kernel.py:132-218).
- * About 3.6 KiB per token plus up to 48 MiB of segment slots (1 MiB each); a
+ * About 2.9 KiB per token plus up to 48 MiB of segment slots (1 MiB each); a
  * larger workspace gives the planner more slots, a smaller one (down to
  * gdn_prefill_workspace_min_bytes) fewer.  Results do not depend on it. */
 size_t gdn_prefill_workspace_bytes(int num_seqs, long long total_tokens);
@@ -107,8 +107,9 @@ int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* st
  * that forbid hipMalloc).  Arguments as gdn_prefill_fwd without the workspace;
  * `stream` must belong to the current device.  Returns GDN_ERR_TOO_LARGE when
  * gdn_prefill_workspace_min_bytes(num_seqs, total_tokens) exceeds the array
- * (about 30k tokens); up to the default workspace size results equal
- * gdn_prefill_fwd's with a default workspace.  Every call on one GPU shares that
+ * (about 145k tokens).  While the default workspace fits in the array (about
+ * 28k tokens) results equal gdn_prefill_fwd's with a default workspace; beyond
+ * that the planner has fewer segment slots and results stay within tolerance.  Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (other streams, other host
  * threads) race and must be ordered by the caller.  Nothing in the array needs
  * to be cleared between calls. */

@@ -19,12 +19,14 @@
 //              smaller batches work-group 0 of the prepass plans and the other
 //              prepass work-groups find their own records.
 //   prepass  : one wave per (record, v-head), or per (record, q/k head) for
-//              large batches, all records in parallel: gates, K K^T / Q K^T on
-//              MFMA, the blocked triangular inverse (diagonal blocks by fp32
-//              forward substitution, the rest on MFMA with bf16 hi + lo
-//              operands), and the packed MFMA operands Tb (fp16), Aqk (bf16)
-//              plus gam / tail, written to the workspace.
-//   consumer : persistent work-groups.  Long sequences are cut into segments
+//              large batches, all records in parallel: gates, K K^T on MFMA,
+//              the blocked triangular inverse (diagonal blocks by fp32 forward
+//              substitution, the rest on MFMA with bf16 hi + lo operands), and
+//              the packed MFMA operand Tb (fp16) plus gam / tail / Gam, written
+//              to the workspace.  It never reads Q.
+//   consumer : persistent work-groups.  Each chunk's Aqk is formed here, from
+//              the K / Q rows in LDS, in tiles shared between the waves through
+//              LDS.  Long sequences are cut into segments
 //              of L chunks (L chosen by the plan); every segment runs at once,
 //              segments >= 1 twice (zero initial state with the real V, and
 //              identity initial state with V = 0), each run split over two
@@ -57,9 +59,11 @@ namespace gdn {
 constexpr int kChunk = 64;
 constexpr int kFragTile = 512;               // one 16x32 MFMA operand fragment: 64 lanes x 8 16-bit values
 // Gate block per (record, v-head): gam[64], tail[64], the chunk's map bound
-// (below) at [128], padding to 256 floats (one 1 KB copy).
+// (below) at [128], Gam[64] (log2 of the cumulative gate, from which the split
+// consumer weights Aqk) at [192] (one 1 KB copy).
 constexpr int kGamStride = 4 * kChunk;
 constexpr int kBoundAt = 2 * kChunk;
+constexpr int kLgamAt = 3 * kChunk;
 // The homogeneous part of one token's update multiplies the state by
 // g_t (I - beta_t k_t k_t^T), whose 2-norm is at most g_t max(1, |1 - beta_t |k_t|^2|).
 // The prepass stores the chunk's sum of log2 of these factors; once a run from
@@ -71,7 +75,7 @@ constexpr float kNegligibleLog2 = -30.0f;
 // as a bf16 hi + lo pair instead of one bf16 (see chain_chunk).
 constexpr float kHiLoBoundLog2 = -8.0f;
 constexpr int kMNegligible = 1 << 30;   // flag in the M-run table: the run stopped early, its map is negligible
-constexpr int kFrags = 2;                    // per (record, v-head): Tb (fp16), Aqk (bf16)
+constexpr int kFrags = 2;                    // per chunk in LDS: Tb (fp16), Aqk (bf16)
 
 // MFMA operands in "permuted fragment order".  For v_mfma_f32_16x16x32_bf16
 // the hardware pairs slot s of lane group lg in A with the same slot of the
@@ -175,8 +179,8 @@ __host__ __device__ inline size_t list_ints(int num_seqs, long long gcap) {
 
 // ---- workspace layout -------------------------------------------------------
 struct WsLayout {
-  size_t frag_off;     // u16  [R][8][2][4096]   (Tb fp16, Aqk bf16)
-  size_t gam_off;      // f32  [R][8][kGamStride] (gam, tail, map bound)
+  size_t frag_off;     // u16  [R][8][kMatElems] Tb (fp16)
+  size_t gam_off;      // f32  [R][8][kGamStride] (gam, tail, map bound, Gam)
   size_t start_off;    // i32  [N + 1]           record start per sequence
   size_t list_off;     // i32  lists (see list_view)
   size_t rec_off;      // i32x4[R]               (seq, first token, length, 0)
@@ -203,7 +207,7 @@ __host__ __device__ inline WsLayout ws_layout(int num_seqs, long long tokens, lo
   const size_t G = static_cast<size_t>(gcap);
   const size_t N = static_cast<size_t>(num_seqs);
   size_t off = 0;
-  L.frag_off = off;  off = align256(off + R * kVHeads * kFrags * kMatElems * sizeof(uint16_t));
+  L.frag_off = off;  off = align256(off + R * kVHeads * kMatElems * sizeof(uint16_t));
   L.gam_off = off;   off = align256(off + R * kVHeads * kGamStride * sizeof(float));
   L.start_off = off; off = align256(off + (N + 1) * sizeof(int));
   L.list_off = off;  off = align256(off + list_ints(num_seqs, static_cast<long long>(G)) * sizeof(int));
@@ -831,23 +835,24 @@ __device__ __forceinline__ void store_frag(const u32x4& x, uint16_t* dst) {
 
 // The terms of NH v-heads (one, or both of a GVA pair, interleaved phase by
 // phase so that their independent latency chains overlap) from the chunk's raw
-// grams: kk[m][n] (n <= m) holds [t = 16 m + 4 lg + rr][i = 16 n + l16] =
-// k_t . k_i; qk[a][m] (a <= m) holds [i = 16 a + 4 lg + rr][t = 16 m + l16] =
-// k_i . q_t.  a_t, b_t: this lane's token (clamped into the chunk) per v-head.
-// The terms go to frag0 / gp0 in the workspace layout: global memory
-// (streamed out), or LDS when kToLds (the direct path).  NB: the number of
-// 16-token blocks that hold tokens (c <= 16 NB).  Later blocks have beta = 0,
-// so their rows of N, their columns of Aqk and every fragment of Tb that
-// touches them are exactly zero: they are stored as zeros without being formed.
+// gram: kk[m][n] (n <= m) holds [t = 16 m + 4 lg + rr][i = 16 n + l16] =
+// k_t . k_i.  a_t, b_t: this lane's token (clamped into the chunk) per v-head.
+// The terms (Tb fragments; gam, tail, the map bound and Gam in the gate block)
+// go to frag0 / gp0 in the workspace layout: global memory (streamed out), or
+// LDS when kToLds (the direct path).  Aqk is formed by the consumers, from the
+// K / Q rows they hold anyway.  NB: the number of 16-token blocks that hold
+// tokens (c <= 16 NB).  Later blocks have beta = 0, so their rows of N and
+// every fragment of Tb that touches them are exactly zero: they are stored as
+// zeros without being formed.
 template <int NH, bool kToLds = false, int NB = 4>
-__device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4], const f32x4 (&qk)[4][4],
+__device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4],
                                               int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
                                               const float (&alog)[kGva], const float (&dtb)[kGva],
                                               uint16_t* __restrict__ frag0, float* __restrict__ gp0) {
   const int lane = threadIdx.x & 63;
   const int l16 = lane & 15, lg = lane >> 4;
   // per-head workspace blocks are consecutive v-heads of one record
-  constexpr size_t kFragStride = static_cast<size_t>(kFrags) * kMatElems;
+  constexpr size_t kFragStride = kMatElems;
 
   // ---- gates: Gam_t = inclusive scan of log2 g (clamped: g = e^-100 is
   // already 0 to fp32 working precision, and a finite floor keeps Gam
@@ -862,6 +867,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     float* gp = gp0 + e * kGamStride;
     gp[lane] = lane < c ? fast_exp2(lgam) : 0.0f;
     gp[kChunk + lane] = lane < c ? fast_exp2(last[e] - lgam) : 0.0f;
+    gp[kLgamAt + lane] = lgam;
     ws.lgam[e][lane] = lgam;
     ws.beta[e][lane] = bet;
   }
@@ -877,33 +883,6 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
       lrow[e][m] = *reinterpret_cast<const f32x4*>(&ws.lgam[e][16 * m + 4 * lg]);
       brow[e][m] = *reinterpret_cast<const f32x4*>(&ws.beta[e][16 * m + 4 * lg]);
     }
-
-  // ---- Aqk = lower(rho . Q K^T), formed transposed: tile (a, m) holds slots
-  // 4 (a & 1) .. + 3 of Aqk fragment (m, a >> 1) ----
-#pragma unroll
-  for (int m = 0; m < 4; ++m) {
-#pragma unroll
-    for (int d = 0; d < 2; ++d) {
-      if (frag_zero(m, d)) continue;
-#pragma unroll
-      for (int e = 0; e < NH; ++e) {
-        float x[8];
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int ai = 2 * d + hf;
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int i = 16 * ai + 4 * lg + rr, t = 16 * m + l16;
-            x[4 * hf + rr] = (ai <= m && m < NB && i <= t)
-                                 ? fast_exp2(lcol[e][m] - lrow[e][ai][rr]) * qk[ai][m][rr] : 0.0f;
-          }
-        }
-        store_frag<kToLds>(
-            u32x4{pack_bf2(x[0], x[1]), pack_bf2(x[2], x[3]), pack_bf2(x[4], x[5]), pack_bf2(x[6], x[7])},
-            frag0 + e * kFragStride + kMatElems + (frag_slot(m, d) * 64 + lane) * 8);
-      }
-    }
-  }
 
   // ---- N = strict_lower(beta_t rho K K^T): diagonal tiles to LDS
   // (column-major) for the substitution, their diagonal |k_t|^2 into the
@@ -1043,41 +1022,34 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
   }
 }
 
-// Raw grams of one chunk (rows t0 .. t0 + c - 1 of q/k head hq), one wave:
-// kk = K K^T (lower tiles, kk[m][n] = [t = 16 m + 4 lg + rr][i = 16 n + l16]),
-// qk = K Q^T (upper tiles, qk[n][m] = [i = 16 n + 4 lg + rr][t = 16 m + l16]).
+// Raw gram of one chunk (rows t0 .. t0 + c - 1 of q/k head hq), one wave:
+// kk = K K^T (lower tiles, kk[m][n] = [t = 16 m + 4 lg + rr][i = 16 n + l16]).
 // Fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
 // columns 32 d + 8 lg .. + 7.  Rows past the chunk end repeat row c - 1: they
-// meet beta = 0 (rows of N), i <= t masks and output rows never stored.
-// Only the tiles of the first NB 16-row blocks are formed.
+// meet beta = 0 (rows of N) and i <= t masks.  Only the tiles of the first NB
+// 16-row blocks are formed.
 template <int NB = 4>
-__device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                            long long t0, int c, int hq, int lane, f32x4 (&kk)[4][4],
-                                            f32x4 (&qk)[4][4]) {
+__device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ k, long long t0, int c, int hq, int lane,
+                                            f32x4 (&kk)[4][4]) {
   const int l16 = lane & 15, lg = lane >> 4;
   const int cm1 = c - 1;
   const uint16_t* krow[NB];
-  const uint16_t* qrow[NB];
 #pragma unroll
   for (int m = 0; m < NB; ++m) {
     const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
     krow[m] = k + (row * kQKHeads + hq) * kDim + 8 * lg;
-    qrow[m] = q + (row * kQKHeads + hq) * kDim + 8 * lg;
   }
 #pragma unroll
   for (int m = 0; m < NB; ++m)
 #pragma unroll
-    for (int n = 0; n <= m; ++n) kk[m][n] = qk[n][m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n <= m; ++n) kk[m][n] = f32x4{0.f, 0.f, 0.f, 0.f};
   // the rows' fragments by depth chunk, two chunks in flight: chunk dd + 2 is
   // loaded into chunk dd's registers once its products are issued (half the
   // operand registers of loading all four at once)
-  bf16x8 kf[2][NB], qf[2][NB];
+  bf16x8 kf[2][NB];
   auto load_dd = [&](int dd) {
 #pragma unroll
-    for (int m = 0; m < NB; ++m) {
-      kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
-      qf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(qrow[m] + 32 * dd);
-    }
+    for (int m = 0; m < NB; ++m) kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
   };
   load_dd(0);
   load_dd(1);
@@ -1086,18 +1058,14 @@ __device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ q, cons
 #pragma unroll
     for (int m = 0; m < NB; ++m)
 #pragma unroll
-      for (int n = 0; n <= m; ++n) {
-        kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
-        qk[n][m] = mfma16(kf[dd & 1][n], qf[dd & 1][m], qk[n][m]);
-      }
+      for (int n = 0; n <= m; ++n) kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
     if (dd + 2 < 4) load_dd(dd + 2);
   }
 }
 
 template <bool kPair>
 __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const float* __restrict__ A_log, const uint16_t* __restrict__ a,
+    const uint16_t* __restrict__ k, const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const int4* __restrict__ recs, const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
     int gcap, int fused_plan, int* __restrict__ rec_start, int* __restrict__ lists,
@@ -1214,8 +1182,8 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
       a_t[e] = e < ne ? bf2f(a[gi + e]) : 0.0f;
       b_t[e] = e < ne ? bf2f(b[gi + e]) : 0.0f;
     }
-    f32x4 kk[4][4], qk[4][4];
-    chunk_grams(q, k, t0, c, hq, lane, kk, qk);
+    f32x4 kk[4][4];
+    chunk_grams(k, t0, c, hq, lane, kk);
 
     const int h0 = kGva * hq + e0;
     float alog[kGva], dtb[kGva];
@@ -1224,14 +1192,14 @@ __global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
       alog[e] = A_log[min(h0 + e, kVHeads - 1)];
       dtb[e] = dt_bias[min(h0 + e, kVHeads - 1)];
     }
-    uint16_t* frag0 = ws_frag + (static_cast<size_t>(r) * kVHeads + h0) * kFrags * kMatElems;
+    uint16_t* frag0 = ws_frag + (static_cast<size_t>(r) * kVHeads + h0) * kMatElems;
     float* gp0 = ws_gam + (static_cast<size_t>(r) * kVHeads + h0) * kGamStride;
     // the v-heads of a pair one after the other (interleaving their phases
     // gains nothing: the phases are VALU-bound, not latency-bound)
     for (int e = 0; e < ne; ++e) {
       const float a1[kGva] = {e == 0 ? a_t[0] : a_t[1], 0.0f}, b1[kGva] = {e == 0 ? b_t[0] : b_t[1], 0.0f};
       const float al1[kGva] = {e == 0 ? alog[0] : alog[1], 0.0f}, dt1[kGva] = {e == 0 ? dtb[0] : dtb[1], 0.0f};
-      prepass_heads<1>(ws, kk, qk, c, a1, b1, al1, dt1, frag0 + e * static_cast<size_t>(kFrags) * kMatElems,
+      prepass_heads<1>(ws, kk, c, a1, b1, al1, dt1, frag0 + e * static_cast<size_t>(kMatElems),
                        gp0 + e * kGamStride);
     }
   }
@@ -1326,6 +1294,28 @@ struct ChunkRef {
   int rec;
 };
 
+// Aqk tile (a, m), a <= m: from the raw tile acc = K_a Q_m^T (C layout: lane
+// (lg, l16) holds rows i = 16 a + 4 lg + rr of column t = 16 m + l16) forms
+// lower(rho . acc), rho[t, i] = 2^(Gam_t - Gam_i), and writes it as slots
+// 4 (a & 1) .. + 3 of Aqk fragment (m, a >> 1) in frag (an LDS Aqk matrix in
+// permuted fragment order).  For even a on the diagonal it also zeroes slots
+// 4-7, which would come from tile (a + 1, m) above the diagonal.  Rows of a
+// partial chunk past its end only reach entries no stored output reads.
+__device__ __forceinline__ void put_aqk_tile(uint16_t* frag, int a, int m, int lane, const f32x4& acc, float gam_t,
+                                             const f32x4& gam_i) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int t = 16 * m + l16;
+  float x[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) x[rr] = 16 * a + 4 * lg + rr <= t ? fast_exp2(gam_t - gam_i[rr]) * acc[rr] : 0.0f;
+  uint16_t* dst = frag + (frag_slot(m, a >> 1) * 64 + lane) * 8 + 4 * (a & 1);
+  const uint32_t h0 = pack_bf2(x[0], x[1]), h1 = pack_bf2(x[2], x[3]);
+  if ((a & 1) == 0 && a == m)
+    *reinterpret_cast<u32x4*>(dst) = u32x4{h0, h1, 0u, 0u};
+  else
+    *reinterpret_cast<u32x2*>(dst) = u32x2{h0, h1};
+}
+
 // Per-thread, chunk-invariant pieces of the operand copies.
 struct DmaLane {
   int row;          // first K / Q / V row this lane copies (then +32 per pass)
@@ -1358,16 +1348,67 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
     dma16<2>(vb + row * (kVHeads * kDim * 2) + dl.v_col, &sm.vs[P][32 * j + 4 * w][0]);   // read once
   }
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
-  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * kFrags * kMatElems);
-  // 12 fragments of 1 KB (Tb then Aqk, contiguous here and in LDS): wave w
-  // copies w and w + 8; waves 4-7 copy their first fragment again (the same
-  // bytes to the same place: branch-free, which keeps this path spill-free)
-  static_assert(kFrags * kMatFrags == 12, "fragment copy split");
-  const int w2 = w < 4 ? w + 8 : w;
-  dma16<2>(fb + (64 * w + lane) * 16, &sm.frag[P][0][0] + 64 * w * 8);   // read once
-  dma16<2>(fb + (64 * w2 + lane) * 16, &sm.frag[P][0][0] + 64 * w2 * 8);
+  const char* fb = reinterpret_cast<const char*>(ws_frag + rh * kMatElems);
+  // the 6 Tb fragments of 1 KB: wave w copies fragment w; waves 6-7 copy
+  // fragments 0-1 again (the same bytes to the same place: branch-free).  The
+  // waves form Aqk themselves (consumer_chunk).
+  static_assert(kMatFrags == 6 && kConsumerWaves == 8, "fragment copy split");
+  const int wf = w < kMatFrags ? w : w - kMatFrags;
+  dma16<2>(fb + (64 * wf + lane) * 16, &sm.frag[P][0][0] + 64 * wf * 8);   // read once
   if (w == 0)   // gam, tail and the map bound: one 1 KB block
     dma16(reinterpret_cast<const char*>(ws_gam + rh * kGamStride) + 16 * lane, &sm.gt[P][0]);
+}
+
+// Full-head consumer wave W's Aqk tiles (a, m) (put_aqk_tile): K row block a
+// for waves 0-1 is 0, for 2-3 is 1, for 4-5 is 2, for 6 is 3; Q row blocks
+// m0 (and m1).  Wave 7 forms none.  Every LDS read is issued before the first
+// product.
+__host__ __device__ constexpr int fh_aqk_a(int w) { return w < 2 ? 0 : w < 4 ? 1 : w < 6 ? 2 : w == 6 ? 3 : -1; }
+__host__ __device__ constexpr int fh_aqk_m0(int w) {
+  return w == 0 ? 0 : w == 1 ? 2 : w == 2 ? 1 : w == 3 ? 3 : w == 4 ? 2 : w < 7 ? 3 : -1;
+}
+__host__ __device__ constexpr int fh_aqk_m1(int w) { return w == 0 ? 1 : w == 1 ? 3 : w == 2 ? 2 : -1; }
+constexpr bool fh_aqk_covers() {   // every tile a <= m exactly once, none above the diagonal
+  int n[4][4] = {};
+  for (int w = 0; w < kConsumerWaves; ++w) {
+    if (fh_aqk_a(w) < 0) continue;
+    ++n[fh_aqk_a(w)][fh_aqk_m0(w)];
+    if (fh_aqk_m1(w) >= 0) ++n[fh_aqk_a(w)][fh_aqk_m1(w)];
+  }
+  for (int a = 0; a < 4; ++a)
+    for (int m = 0; m < 4; ++m)
+      if (n[a][m] != (a <= m ? 1 : 0)) return false;
+  return true;
+}
+static_assert(fh_aqk_covers(), "full-head Aqk tiles");
+
+template <int W, int P>
+__device__ __forceinline__ void fh_aqk(ConsumerSmem& sm, int lane) {
+  constexpr int a = fh_aqk_a(W), m0 = fh_aqk_m0(W), m1 = fh_aqk_m1(W);
+  if constexpr (a >= 0) {
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int rsw = kq_swz(l16);
+    bf16x8 kb[4], q0[4], q1[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const int at = 8 * ((4 * d + lg) ^ rsw);
+      kb[d] = *reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * a + l16][at]);
+      q0[d] = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m0 + l16][at]);
+      if constexpr (m1 >= 0) q1[d] = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m1 + l16][at]);
+    }
+    const f32x4 gi = *reinterpret_cast<const f32x4*>(&sm.gt[P][kLgamAt + 16 * a + 4 * lg]);
+    const float g0 = sm.gt[P][kLgamAt + 16 * m0 + l16];
+    const float g1 = sm.gt[P][kLgamAt + 16 * (m1 >= 0 ? m1 : m0) + l16];
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      acc0 = mfma16(kb[d], q0[d], acc0);
+      if constexpr (m1 >= 0) acc1 = mfma16(kb[d], q1[d], acc1);
+    }
+    put_aqk_tile(&sm.frag[P][1][0], a, m0, lane, acc0, g0, gi);
+    if constexpr (m1 >= 0) put_aqk_tile(&sm.frag[P][1][0], a, m1, lane, acc1, g1, gi);
+  }
 }
 
 // One chunk of the recurrence for the 16-wide V tile of this wave.
@@ -1380,10 +1421,22 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
 //         (num_records = c rows, so stores of rows t >= c are dropped by the
 //         range check: no branch); ocol = byte offset of value column v0 + 4 lg.
 template <int P>
-__device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f32x4 (&st)[8], int w,
+__device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&st)[8], int w,
                                                int lane, float scale, __amdgpu_buffer_rsrc_t orc,
                                                uint32_t ocol) {
   const int l16 = lane & 15, lg = lane >> 4;
+  // ---- this wave's Aqk tiles, first (fewest registers live); every wave
+  // reads them after the barrier before O^T ----
+  switch (w) {   // uniform
+    case 0: fh_aqk<0, P>(sm, lane); break;
+    case 1: fh_aqk<1, P>(sm, lane); break;
+    case 2: fh_aqk<2, P>(sm, lane); break;
+    case 3: fh_aqk<3, P>(sm, lane); break;
+    case 4: fh_aqk<4, P>(sm, lane); break;
+    case 5: fh_aqk<5, P>(sm, lane); break;
+    case 6: fh_aqk<6, P>(sm, lane); break;
+    default: break;
+  }
   f32x4 gam[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) gam[m] = *reinterpret_cast<const f32x4*>(&sm.gt[P][16 * m + 4 * lg]);
@@ -1413,6 +1466,7 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
       YT[m] = mfma16(sb[d], qa, YT[m]);
     }
   }
+
 
   // ---- R = V - gam X (V columns by transposed LDS reads), Delta = Tb R ----
   // lane (lg, l16) addresses row 16m + 4lg + l16/4, columns 16w + 4(l16 & 3) .. +3
@@ -1472,6 +1526,7 @@ __device__ __forceinline__ void consumer_chunk(const ConsumerSmem& sm, int c, f3
 
   // ---- O^T = scale (Y^T diag(gam) + Delta^T Aqk^T): lane (lg, l16) holds token
   //      16m + l16, value columns 4lg .. 4lg+3 -> one 8-byte store ----
+  lds_barrier();   // every wave's Aqk tiles are in LDS
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     f32x4 OT = {0.f, 0.f, 0.f, 0.f};
@@ -1730,9 +1785,9 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
     // only the 16-token blocks that hold tokens are formed (c <= 16 nb)
     auto blocks = [&](auto NBC) {
       constexpr int NB = decltype(NBC)::value;
-      f32x4 kk[4][4], qk[4][4];
-      chunk_grams<NB>(q, k, c0, c, hq, lane, kk, qk);
-      prepass_heads<1, true, NB>(sm.w[J], kk, qk, c, a1, b1, al1, dt1, &sm.c.frag[J][0][0], &sm.c.gt[J][0]);
+      f32x4 kk[4][4];
+      chunk_grams<NB>(k, c0, c, hq, lane, kk);
+      prepass_heads<1, true, NB>(sm.w[J], kk, c, a1, b1, al1, dt1, &sm.c.frag[J][0][0], &sm.c.gt[J][0]);
     };
     switch ((c + 15) >> 4) {
       case 1: blocks(std::integral_constant<int, 1>{}); break;
@@ -1851,11 +1906,11 @@ __device__ __forceinline__ void split_dma(SplitSmem& sm, const ChunkRef& cr, con
 #pragma unroll
   for (int j = 0; j < 2; ++j) dma16_buf<2>(vr, dl.v[j], &sm.vs[P][32 * j + 8 * ws][0]);   // V: read once
   const size_t rh = static_cast<size_t>(cr.rec) * kVHeads + h;
-  // 12 fragments of 1 KB (Tb then Aqk): side wave ws copies ws, ws + 4, ws + 8
-  const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kFrags * kMatElems, kFrags * kMatElems * 2);
-#pragma unroll
-  for (int j = 0; j < kFrags * kMatFrags / 4; ++j)
-    dma16_buf(fr, dl.fr + 4096u * j, &sm.frag[P][0][0] + (256 * j + 64 * ws) * 8);
+  // the 6 Tb fragments of 1 KB: side wave ws copies ws and ws + 4 (< 6); the
+  // side waves form Aqk themselves
+  const __amdgpu_buffer_rsrc_t fr = buf_rsrc(ws_frag + rh * kMatElems, kMatElems * 2);
+  dma16_buf(fr, dl.fr, &sm.frag[P][0][0] + 64 * ws * 8);
+  if (ws + 4 < kMatFrags) dma16_buf(fr, dl.fr + 4096u, &sm.frag[P][0][0] + (256 + 64 * ws) * 8);
   if (ws == 0) dma16_buf(buf_rsrc(ws_gam + rh * kGamStride, kGamStride * 4), dl.g, &sm.gt[P][0]);
 }
 
@@ -2051,45 +2106,107 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   for (int d = 0; d < 4; ++d) sm.sbx[w][d][lane] = __builtin_bit_cast(u32x4, nb[d]);
 }
 
+// The side wave that forms Aqk tile (a, m) (K row block a, Q row block m,
+// a <= m): the ten tiles in row order go 3 / 3 / 2 / 2 to side waves 0-3, so
+// no wave needs more than two K row blocks.
+__host__ __device__ constexpr int aqk_owner(int a, int m) {
+  const int idx = 4 * a - a * (a - 1) / 2 + (m - a);
+  return idx < 3 ? 0 : idx < 6 ? 1 : idx < 8 ? 2 : 3;
+}
+constexpr bool aqk_owner_blocks() {   // side wave w's tiles use K row blocks max(w - 1, 0) and w only
+  for (int a = 0; a < 4; ++a)
+    for (int m = a; m < 4; ++m) {
+      const int w = aqk_owner(a, m);
+      if (w < 0 || w > 3 || (a != w && a != (w > 0 ? w - 1 : 0))) return false;
+    }
+  return true;
+}
+static_assert(aqk_owner_blocks(), "Aqk tile owners");
+
+// Side wave WS, first half of a chunk: Y^T = S Q^T for chain wave WS's tile,
+// and the wave's Aqk tiles (put_aqk_tile).  One straight-line body per wave:
+// every LDS read is issued before the first product, and the Y^T and Aqk
+// products interleave.
+template <int WS, int P>
+__device__ __forceinline__ void side_front(SplitSmem& sm, int lane, f32x4 (&YT)[4]) {
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int rsw = kq_swz(l16);
+  constexpr int a_lo = WS > 0 ? WS - 1 : 0;   // the K row blocks this wave's tiles use
+  constexpr int a_hi = WS;
+  bf16x8 sb[4], qa[4][4], kb[2][4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    sb[d] = __builtin_bit_cast(bf16x8, sm.sbx[WS][d][lane]);
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+      qa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int a = j == 0 ? a_lo : a_hi;
+      if (j == 0 || a_hi != a_lo)
+        kb[j][d] = *reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * a + l16][8 * ((4 * d + lg) ^ rsw)]);
+    }
+  }
+  f32x4 gi[2];
+  gi[0] = *reinterpret_cast<const f32x4*>(&sm.gt[P][kLgamAt + 16 * a_lo + 4 * lg]);
+  gi[1] = *reinterpret_cast<const f32x4*>(&sm.gt[P][kLgamAt + 16 * a_hi + 4 * lg]);
+  float gtm[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) gtm[m] = sm.gt[P][kLgamAt + 16 * m + l16];
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc[2][4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) YT[m] = mfma16(sb[d], qa[d][m], YT[m]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int a = j == 0 ? a_lo : a_hi;
+        if ((j == 1 && a_hi == a_lo) || m < a || aqk_owner(a, m) != WS) continue;
+        acc[j][m] = mfma16(kb[j][d], qa[d][m], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j][m]);
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int a = j == 0 ? a_lo : a_hi;
+      if ((j == 1 && a_hi == a_lo) || m < a || aqk_owner(a, m) != WS) continue;
+      put_aqk_tile(&sm.frag[P][1][0], a, m, lane, acc[j][m], gtm[m], gi[j]);
+    }
+}
+
 // Side wave, one chunk: outputs of the chunk (tile of chain wave ws).
 template <int P, typename Copy>
 __device__ __forceinline__ void side_chunk(SplitSmem& sm, int ws, int lane, float scale,
                                            __amdgpu_buffer_rsrc_t orc, uint32_t ocol, Copy&& copy_next) {
-  const int l16 = lane & 15, lg = lane >> 4;
+  const int l16 = lane & 15;
   // the copies go first: they then have the whole chunk to land, and Y^T runs
   // while the chain wave is in its VALU-heavy R / Delta phase instead of X
   copy_next();
-  const int rsw = kq_swz(l16);
-  bf16x8 sb[4], qa[4][4];
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    sb[d] = __builtin_bit_cast(bf16x8, sm.sbx[ws][d][lane]);
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-      qa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * m + l16][8 * ((4 * d + lg) ^ rsw)]);
-  }
-  __builtin_amdgcn_sched_barrier(0);
   f32x4 YT[4];
-#pragma unroll
-  for (int m = 0; m < 4; ++m) YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int d = 0; d < 4; ++d)
-#pragma unroll
-    for (int m = 0; m < 4; ++m) YT[m] = mfma16(sb[d], qa[d][m], YT[m]);
-  // Aqk fragments and gates of the output phase
-  bf16x8 fa[2][4];
+  switch (ws) {   // uniform
+    case 0: side_front<0, P>(sm, lane, YT); break;
+    case 1: side_front<1, P>(sm, lane, YT); break;
+    case 2: side_front<2, P>(sm, lane, YT); break;
+    default: side_front<3, P>(sm, lane, YT); break;
+  }
   float sg[4];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < 4; ++m) sg[m] = scale * sm.gt[P][16 * m + l16];
+  lds_barrier();   // B2: Delta fragments and every side wave's Aqk tiles visible
+  bf16x8 dob[2], fa[2][4];
+#pragma unroll
+  for (int d = 0; d < 2; ++d) dob[d] = __builtin_bit_cast(bf16x8, sm.dox[ws][d][lane]);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int d = 0; d < 2; ++d)
       if (!frag_zero(m, d)) fa[d][m] = *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][(frag_slot(m, d) * 64 + lane) * 8]);
-    sg[m] = scale * sm.gt[P][16 * m + l16];
-  }
-  lds_barrier();   // B2
-  bf16x8 dob[2];
-#pragma unroll
-  for (int d = 0; d < 2; ++d) dob[d] = __builtin_bit_cast(bf16x8, sm.dox[ws][d][lane]);
   __builtin_amdgcn_sched_barrier(0);
   f32x4 OT[4];
 #pragma unroll
@@ -2687,13 +2804,13 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
   if (R * kVHeads <= kPrepassMaxGroups * kPrepassWaves) {
     const long long g_pre = (R * kVHeads + kPrepassWaves - 1) / kPrepassWaves;
     prepass_kernel<false><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
-        qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
+        kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
         Ri, gc, fused_plan, rec_start, lists, frag, gam);
   } else {
     const long long g_pre =
         std::min<long long>((R * kQKHeads + kPrepassWaves - 1) / kPrepassWaves, kPrepassMaxGroups);
     prepass_kernel<true><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
-        qb, kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
+        kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
         Ri, gc, fused_plan, rec_start, lists, frag, gam);
   }
   // persistent grids: one work-group per CU per consumer kind at most; a

@@ -59,7 +59,7 @@ def test_workspace_size_c3_and_growth(lib):
     # configuration 3 (16 sequences, 16384 tokens): the default workspace stays
     # below the call's own algorithmic traffic (117,964,864 bytes)
     assert lib.gdn_prefill_workspace_bytes(16, 16384) <= 117_964_864
-    # about 3.6 KiB per token beyond the default slots, not the ~10 KiB per
+    # about 2.9 KiB per token beyond the default slots, not the ~10 KiB per
     # token of slots sized for the shortest segments
     big = lib.gdn_prefill_workspace_bytes(1, 1 << 20)
     assert big <= (1 << 20) * 3800 + (64 << 20), big
