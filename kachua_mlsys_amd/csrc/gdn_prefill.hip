@@ -1382,10 +1382,14 @@ constexpr bool fh_aqk_covers() {   // every tile a <= m exactly once, none above
 }
 static_assert(fh_aqk_covers(), "full-head Aqk tiles");
 
+// Tiles of Q row blocks at or past the chunk length c feed only output rows
+// that are never stored: they are skipped (m1 > m0, so m0's test covers both).
 template <int W, int P>
-__device__ __forceinline__ void fh_aqk(ConsumerSmem& sm, int lane) {
+__device__ __forceinline__ void fh_aqk(ConsumerSmem& sm, int lane, int c) {
   constexpr int a = fh_aqk_a(W), m0 = fh_aqk_m0(W), m1 = fh_aqk_m1(W);
+  static_assert(m1 < 0 || m1 > m0, "tile order");
   if constexpr (a >= 0) {
+    if (16 * m0 >= c) return;   // uniform
     const int l16 = lane & 15, lg = lane >> 4;
     const int rsw = kq_swz(l16);
     bf16x8 kb[4], q0[4], q1[4];
@@ -1407,7 +1411,8 @@ __device__ __forceinline__ void fh_aqk(ConsumerSmem& sm, int lane) {
       if constexpr (m1 >= 0) acc1 = mfma16(kb[d], q1[d], acc1);
     }
     put_aqk_tile(&sm.frag[P][1][0], a, m0, lane, acc0, g0, gi);
-    if constexpr (m1 >= 0) put_aqk_tile(&sm.frag[P][1][0], a, m1, lane, acc1, g1, gi);
+    if constexpr (m1 >= 0)
+      if (16 * m1 < c) put_aqk_tile(&sm.frag[P][1][0], a, m1, lane, acc1, g1, gi);
   }
 }
 
@@ -1428,13 +1433,13 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
   // ---- this wave's Aqk tiles, first (fewest registers live); every wave
   // reads them after the barrier before O^T ----
   switch (w) {   // uniform
-    case 0: fh_aqk<0, P>(sm, lane); break;
-    case 1: fh_aqk<1, P>(sm, lane); break;
-    case 2: fh_aqk<2, P>(sm, lane); break;
-    case 3: fh_aqk<3, P>(sm, lane); break;
-    case 4: fh_aqk<4, P>(sm, lane); break;
-    case 5: fh_aqk<5, P>(sm, lane); break;
-    case 6: fh_aqk<6, P>(sm, lane); break;
+    case 0: fh_aqk<0, P>(sm, lane, c); break;
+    case 1: fh_aqk<1, P>(sm, lane, c); break;
+    case 2: fh_aqk<2, P>(sm, lane, c); break;
+    case 3: fh_aqk<3, P>(sm, lane, c); break;
+    case 4: fh_aqk<4, P>(sm, lane, c); break;
+    case 5: fh_aqk<5, P>(sm, lane, c); break;
+    case 6: fh_aqk<6, P>(sm, lane, c); break;
     default: break;
   }
   f32x4 gam[4];
@@ -1952,19 +1957,10 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   const int vrow = 4 * lg + (l16 >> 2);
   const int vat = 8 * ((2 * w + ((l16 & 3) >> 1)) ^ vh_swz(vrow)) + 4 * (l16 & 1);
 
-  // ---- X = K S^T.  S enters as one bf16, plus its bf16 rounding residue
-  // in a second pass when the chunk's map bound says the state barely decays:
-  // then the rounding of S here is what accumulates over a long sequence
-  // (single bf16: state error 1.2e-3 to 1.5e-3 at 4k to 28k tokens of near-1
-  // decay; hi + lo: 3e-4 to 4e-4).  Where the map contracts by 2^-8 or more
-  // per chunk, earlier roundings do not accumulate and one bf16 suffices.
-  // The K fragments are read in two batches of eight and the products of a
-  // depth chunk start once its fragments have landed (at most 15 LDS reads
-  // can be waited for individually); the bound, read first, is tested after
-  // the first pass.
   // ---- the diagonal Aqk tile (w, w) (put_aqk_tile), first: few registers
-  // are live here; the side waves form the tiles below the diagonal ----
-  {
+  // are live here; the side waves form the tiles below the diagonal.  A tile
+  // at or past the chunk length feeds only output rows never stored. ----
+  if (16 * w < c) {   // uniform
     bf16x8 kd[4], qd[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -1979,6 +1975,17 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
     put_aqk_tile(&sm.frag[P][1][0], w, w, lane, adiag, gdt, gdi);
   }
   __builtin_amdgcn_sched_barrier(0);
+
+  // ---- X = K S^T.  S enters as one bf16, plus its bf16 rounding residue
+  // in a second pass when the chunk's map bound says the state barely decays:
+  // then the rounding of S here is what accumulates over a long sequence
+  // (single bf16: state error 1.2e-3 to 1.5e-3 at 4k to 28k tokens of near-1
+  // decay; hi + lo: 3e-4 to 4e-4).  Where the map contracts by 2^-8 or more
+  // per chunk, earlier roundings do not accumulate and one bf16 suffices.
+  // The K fragments are read in two batches of eight and the products of a
+  // depth chunk start once its fragments have landed (at most 15 LDS reads
+  // can be waited for individually); the bound, read first, is tested after
+  // the first pass.
   const float cbound = sm.gt[P][kBoundAt];   // first LDS read: done before the first K fragment
   bf16x8 ka[4][4];
   auto read_k = [&](int d) {
