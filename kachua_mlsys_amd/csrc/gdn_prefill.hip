@@ -1957,25 +1957,6 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   const int vrow = 4 * lg + (l16 >> 2);
   const int vat = 8 * ((2 * w + ((l16 & 3) >> 1)) ^ vh_swz(vrow)) + 4 * (l16 & 1);
 
-  // ---- the diagonal Aqk tile (w, w) (put_aqk_tile), first: few registers
-  // are live here; the side waves form the tiles below the diagonal.  A tile
-  // at or past the chunk length feeds only output rows never stored. ----
-  if (16 * w < c) {   // uniform
-    bf16x8 kd[4], qd[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      kd[d] = *reinterpret_cast<const bf16x8*>(&sm.ks[P][16 * w + l16][8 * ((4 * d + lg) ^ rsw)]);
-      qd[d] = *reinterpret_cast<const bf16x8*>(&sm.qs[P][16 * w + l16][8 * ((4 * d + lg) ^ rsw)]);
-    }
-    const f32x4 gdi = *reinterpret_cast<const f32x4*>(&sm.gt[P][kLgamAt + 16 * w + 4 * lg]);
-    const float gdt = sm.gt[P][kLgamAt + 16 * w + l16];
-    f32x4 adiag = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int d = 0; d < 4; ++d) adiag = mfma16(kd[d], qd[d], adiag);
-    put_aqk_tile(&sm.frag[P][1][0], w, w, lane, adiag, gdt, gdi);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-
   // ---- X = K S^T.  S enters as one bf16, plus its bf16 rounding residue
   // in a second pass when the chunk's map bound says the state barely decays:
   // then the rounding of S here is what accumulates over a long sequence
@@ -2021,7 +2002,6 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int m = 0; m < 4; ++m) X[m] = mfma16(ka[3][m], sb[3], X[m]);
-
   if (cbound > kHiLoBoundLog2) {   // uniform
     bf16x8 sbl[4];
     state_frags_lo(st, sb, sbl);
@@ -2100,7 +2080,7 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
     gather_slots(D, d, x);
     sm.dox[w][d][lane] = __builtin_bit_cast(u32x4, round_frag(x));
   }
-  lds_barrier();   // B2: Delta fragments and the Aqk tiles visible to the side waves (and S fragments consumed)
+  lds_barrier();   // B2: Delta fragments visible to the side wave (and S fragments consumed)
 
   // ---- Delta' = tail Delta (hi + lo); S^T <- gam_c S^T + K^T Delta' ----
   bf16x8 dh[2], dl[2];
@@ -2131,24 +2111,20 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   for (int d = 0; d < 4; ++d) sm.sbx[w][d][lane] = __builtin_bit_cast(u32x4, nb[d]);
 }
 
-// Who forms Aqk tile (a, m) (K row block a, Q row block m, a <= m) in the
-// split consumer: chain wave a forms the diagonal tile (a, a); the six tiles
-// below it go 2 / 2 / 1 / 1 to side waves 0-3 (aqk_owner; -1 on the diagonal),
-// which then need K row blocks side_a_lo(w) .. side_a_hi(w) only.
+// The side wave that forms Aqk tile (a, m) (K row block a, Q row block m,
+// a <= m): the ten tiles in row order go 3 / 3 / 2 / 2 to side waves 0-3, so
+// no wave needs more than two K row blocks.
 __host__ __device__ constexpr int aqk_owner(int a, int m) {
-  return a == m ? -1 : a == 0 ? (m < 3 ? 0 : 1) : a == 1 ? (m == 2 ? 1 : 2) : 3;
+  const int idx = 4 * a - a * (a - 1) / 2 + (m - a);
+  return idx < 3 ? 0 : idx < 6 ? 1 : idx < 8 ? 2 : 3;
 }
-__host__ __device__ constexpr int side_a_lo(int w) { return w < 2 ? 0 : w - 1; }
-__host__ __device__ constexpr int side_a_hi(int w) { return w == 0 ? 0 : w - 1 + (w == 1 ? 1 : 0); }
-constexpr bool aqk_owner_blocks() {   // every tile below the diagonal once, within its wave's K blocks
-  int n[4] = {0, 0, 0, 0};
+constexpr bool aqk_owner_blocks() {   // side wave w's tiles use K row blocks max(w - 1, 0) and w only
   for (int a = 0; a < 4; ++a)
-    for (int m = a + 1; m < 4; ++m) {
+    for (int m = a; m < 4; ++m) {
       const int w = aqk_owner(a, m);
-      if (w < 0 || w > 3 || a < side_a_lo(w) || a > side_a_hi(w)) return false;
-      ++n[w];
+      if (w < 0 || w > 3 || (a != w && a != (w > 0 ? w - 1 : 0))) return false;
     }
-  return n[0] + n[1] + n[2] + n[3] == 6 && aqk_owner(2, 2) == -1;
+  return true;
 }
 static_assert(aqk_owner_blocks(), "Aqk tile owners");
 
@@ -2160,8 +2136,8 @@ template <int WS, int P>
 __device__ __forceinline__ void side_front(SplitSmem& sm, int lane, f32x4 (&YT)[4]) {
   const int l16 = lane & 15, lg = lane >> 4;
   const int rsw = kq_swz(l16);
-  constexpr int a_lo = side_a_lo(WS);   // the K row blocks this wave's tiles use
-  constexpr int a_hi = side_a_hi(WS);
+  constexpr int a_lo = WS > 0 ? WS - 1 : 0;   // the K row blocks this wave's tiles use
+  constexpr int a_hi = WS;
   bf16x8 sb[4], qa[4][4], kb[2][4];
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
@@ -2195,7 +2171,7 @@ __device__ __forceinline__ void side_front(SplitSmem& sm, int lane, f32x4 (&YT)[
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int a = j == 0 ? a_lo : a_hi;
-        if ((j == 1 && a_hi == a_lo) || m <= a || aqk_owner(a, m) != WS) continue;
+        if ((j == 1 && a_hi == a_lo) || m < a || aqk_owner(a, m) != WS) continue;
         acc[j][m] = mfma16(kb[j][d], qa[d][m], d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j][m]);
       }
   }
@@ -2204,7 +2180,7 @@ __device__ __forceinline__ void side_front(SplitSmem& sm, int lane, f32x4 (&YT)[
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int a = j == 0 ? a_lo : a_hi;
-      if ((j == 1 && a_hi == a_lo) || m <= a || aqk_owner(a, m) != WS) continue;
+      if ((j == 1 && a_hi == a_lo) || m < a || aqk_owner(a, m) != WS) continue;
       put_aqk_tile(&sm.frag[P][1][0], a, m, lane, acc[j][m], gtm[m], gi[j]);
     }
 }
