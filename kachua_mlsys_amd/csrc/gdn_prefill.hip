@@ -739,10 +739,11 @@ __device__ __forceinline__ void lds_barrier() {
 // of a row per lane is both the A and the B fragment of a gram), the gates sit
 // on the lanes (lane = token), and only the 16x16 diagonal blocks of the
 // triangular inverse pass through LDS.  An item is one (record, v-head) when
-// the batch has at most 2048 of them (each v-head's phases on its own wave:
-// the shortest latency for a lone item), else one (record, q/k head) whose
-// wave loads the rows and forms the grams once and runs both v-heads of the
-// GVA pair (two waves per SIMD: up to 512 records at once).
+// the batch has at most 3072 of them (each v-head's phases on its own wave:
+// the shortest latency; two waves per SIMD up to 2048 items, three beyond),
+// else one (record, q/k head) whose wave loads the rows and forms the gram
+// once and runs both v-heads of the GVA pair (two waves per SIMD: up to 512
+// records at once).
 //
 // The inverse is formed transposed: with U = I + N^T (unit upper) and
 // W = U^{-1} = T^T, the 16x16 blocks satisfy
@@ -1063,8 +1064,10 @@ __device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ k, long
   }
 }
 
-template <bool kPair>
-__global__ __launch_bounds__(kPrepassThreads, 2) void prepass_kernel(
+// kGroups: work-groups per CU the register budget is sized for (2, or 3 for
+// one-v-head items in batches of 2048-3072 of them).
+template <bool kPair, int kGroups>
+__global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
     const uint16_t* __restrict__ k, const float* __restrict__ A_log, const uint16_t* __restrict__ a,
     const float* __restrict__ dt_bias, const uint16_t* __restrict__ b,
     const int4* __restrict__ recs, const void* __restrict__ cu, int is64, int num_seqs, long long T, int R,
@@ -2803,18 +2806,26 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
   if (!fused_plan)
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
                                                         total_tokens, Ri, gc, rec_start, recs, lists);
-  // one wave per (record, v-head) for small batches (a lone item's latency
-  // matters there), else one per (record, q/k head): then the grams and the K /
-  // Q loads are not repeated per v-head, and up to 512 records start at once
-  if (R * kVHeads <= kPrepassMaxGroups * kPrepassWaves) {
-    const long long g_pre = (R * kVHeads + kPrepassWaves - 1) / kPrepassWaves;
-    prepass_kernel<false><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
+  // one wave per (record, v-head) while every item fits in one round: two
+  // waves per SIMD for up to 2048 items (a lone item's latency matters there),
+  // three (a tighter register budget) for up to 3072.  Larger batches take one
+  // wave per (record, q/k head): the gram and the K loads are then not
+  // repeated per v-head, and up to 512 records start at once.
+  const long long items_v = R * kVHeads;
+  if (items_v <= kPrepassMaxGroups * kPrepassWaves) {
+    const long long g_pre = (items_v + kPrepassWaves - 1) / kPrepassWaves;
+    prepass_kernel<false, 2><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
+        kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
+        Ri, gc, fused_plan, rec_start, lists, frag, gam);
+  } else if (items_v <= 3 * (kPrepassMaxGroups / 2) * kPrepassWaves) {
+    const long long g_pre = (items_v + kPrepassWaves - 1) / kPrepassWaves;
+    prepass_kernel<false, 3><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
         kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
         Ri, gc, fused_plan, rec_start, lists, frag, gam);
   } else {
     const long long g_pre =
         std::min<long long>((R * kQKHeads + kPrepassWaves - 1) / kPrepassWaves, kPrepassMaxGroups);
-    prepass_kernel<true><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
+    prepass_kernel<true, 2><<<dim3(static_cast<unsigned>(g_pre + fused_plan)), dim3(kPrepassThreads), 0, st>>>(
         kb, A_log, ab, dt_bias, bb, recs, cu_seqlens, cu_seqlens_is_int64, num_seqs, total_tokens,
         Ri, gc, fused_plan, rec_start, lists, frag, gam);
   }
