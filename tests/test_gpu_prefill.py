@@ -42,6 +42,22 @@ def test_prefill_ragged(gpu, lengths):
            f"prefill ragged {lengths}")
 
 
+# Chunk lengths on both sides of every 16-token block boundary.  The consumers
+# form Aqk in 16x16 tiles and skip tiles past a chunk's last token: sequences
+# of at most one chunk run on the full-head consumer, the longer ones end in a
+# partial chunk on the split consumer (the batch is too large for the direct
+# path).
+def test_prefill_partial_chunk_blocks(gpu):
+    tails = [1, 15, 16, 17, 31, 32, 33, 47, 48, 49, 63, 64]
+    lengths = tails + [128 * (i + 1) + t for i, t in enumerate(tails)]
+    _check(prefill_inputs_from_lengths(lengths, seed=77), gpu, "partial chunk blocks")
+    # the same with near-1 decay: the state's lo pass and segment maps that
+    # stay large, so the finish corrects every later segment
+    p = prefill_inputs_from_lengths(lengths, seed=78)
+    p.A_log = torch.linspace(-8.0, -5.0, 8)
+    _check(p, gpu, "partial chunk blocks, weak decay")
+
+
 @pytest.mark.parametrize("lengths,zero_state,cu64", [
     ([16], False, False), ([64], True, False), ([10, 0, 20, 34], False, True), ([1] * 64, False, False),
     ([0, 0, 0, 5, 0], True, True), ([0, 0], False, False), ([128], False, False), ([100, 28], False, True),
