@@ -1221,8 +1221,9 @@ constexpr int kConsumerThreads = 64 * kConsumerWaves;
 //             is stored at position j ^ kq_swz(t) (row reads conflict-free,
 //             transposed reads at two passes per 32 lanes).
 //   vs      : V rows; chunk j of row t at j ^ v_swz(t).
-//   frag    : Tb (fp16), Aqk (bf16) in permuted fragment order (lane-contiguous).
-//   gt      : gam[64], tail[64] and 128 floats of padding.
+//   frag    : Tb (fp16, copied) and Aqk (bf16, formed by the waves) in
+//             permuted fragment order (lane-contiguous).
+//   gt      : the gate block: gam[64], tail[64], the map bound, Gam[64].
 // Rows t >= c of a partial chunk hold copies of row c-1 (finite data) or
 // zeros; they only meet zero rows / columns of Tb and Aqk and zero gam / tail.
 struct __align__(16) ConsumerSmem {
@@ -1827,8 +1828,8 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
 // so the time per chunk bounds the whole call.  Each 16-wide value tile gets
 // two waves on one SIMD: the chain wave (waves 0-3) carries the state through
 // X = K S^T, R, Delta = Tb R and S' = gam_c S + K^T Delta'; the side wave
-// (waves 4-7) forms the outputs (Y^T = S Q^T, O^T = Delta^T Aqk^T, stores) and
-// copies the next chunk's operands.  The chain wave hands S and Delta (bf16
+// (waves 4-7) forms the chunk's Aqk tiles and the outputs (Y^T = S Q^T,
+// O^T = Delta^T Aqk^T, stores) and copies the next chunk's operands.  The chain wave hands S and Delta (bf16
 // fragments, in its own register order) to its side wave through LDS, so the
 // side wave's MFMAs and VALU work run in the gaps of the chain's dependent
 // MFMA sequence.  Two barriers per chunk: B2 (Delta ready; waits for LDS
