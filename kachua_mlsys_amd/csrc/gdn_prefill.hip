@@ -1359,7 +1359,7 @@ __device__ __forceinline__ void dma_chunk(ConsumerSmem& sm, const ChunkRef& cr, 
   static_assert(kMatFrags == 6 && kConsumerWaves == 8, "fragment copy split");
   const int wf = w < kMatFrags ? w : w - kMatFrags;
   dma16<2>(fb + (64 * wf + lane) * 16, &sm.frag[P][0][0] + 64 * wf * 8);   // read once
-  if (w == 0)   // gam, tail and the map bound: one 1 KB block
+  if (w == 0)   // the gate block (gam, tail, the map bound, Gam): 1 KB
     dma16(reinterpret_cast<const char*>(ws_gam + rh * kGamStride) + 16 * lane, &sm.gt[P][0]);
 }
 
@@ -1475,7 +1475,6 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
       YT[m] = mfma16(sb[d], qa, YT[m]);
     }
   }
-
 
   // ---- R = V - gam X (V columns by transposed LDS reads), Delta = Tb R ----
   // lane (lg, l16) addresses row 16m + 4lg + l16/4, columns 16w + 4(l16 & 3) .. +3
@@ -1829,12 +1828,13 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
 // two waves on one SIMD: the chain wave (waves 0-3) carries the state through
 // X = K S^T, R, Delta = Tb R and S' = gam_c S + K^T Delta'; the side wave
 // (waves 4-7) forms the chunk's Aqk tiles and the outputs (Y^T = S Q^T,
-// O^T = Delta^T Aqk^T, stores) and copies the next chunk's operands.  The chain wave hands S and Delta (bf16
-// fragments, in its own register order) to its side wave through LDS, so the
-// side wave's MFMAs and VALU work run in the gaps of the chain's dependent
-// MFMA sequence.  Two barriers per chunk: B2 (Delta ready; waits for LDS
-// traffic only, so the operand copies, issued at the chunk's start, stay in
-// flight) and B3 at the chunk's end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
+// O^T = Delta^T Aqk^T, stores) and copies the next chunk's operands.  The
+// chain wave hands S and Delta (bf16 fragments, in its own register order) to
+// its side wave through LDS, so the side wave's MFMAs and VALU work run in the
+// gaps of the chain's dependent MFMA sequence.  Two barriers per chunk: B2
+// (Delta and the Aqk tiles ready; waits for LDS traffic only, so the operand
+// copies, issued at the chunk's start, stay in flight) and B3 at the chunk's
+// end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
 // side wave reads them before B2 of chunk i+1, so one buffer suffices.
 constexpr int kSplitThreads = 512;
 constexpr int kHalfV = 64;                 // value rows per split work-group (4 tiles)
