@@ -1834,10 +1834,34 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
 // gaps of the chain's dependent MFMA sequence.  Two barriers per chunk: B2
 // (Delta and the Aqk tiles ready; waits for LDS traffic only, so the operand
 // copies, issued at the chunk's start, stay in flight) and B3 at the chunk's
-// end.  The S fragments of chunk i+1 are written after B2 of chunk i, and the
-// side wave reads them before B2 of chunk i+1, so one buffer suffices.
+// end (see split_barrier).  The S fragments of chunk i+1 are written after
+// B2 of chunk i, and the side wave reads them before B2 of chunk i+1, so one
+// buffer suffices.
 constexpr int kSplitThreads = 512;
 constexpr int kHalfV = 64;                 // value rows per split work-group (4 tiles)
+constexpr int kSideStores = 4;             // output stores a side wave issues per chunk, after its copies
+static_assert(kSideStores == kChunk / 16, "side_chunk stores one 8-byte row piece per 16-token block");
+
+// Barrier of the split consumer: every wave's LDS writes are visible, and each
+// side wave has at most kPending vector memory operations outstanding.  The
+// chain waves issue no vector memory operation a later phase depends on: their
+// state loads are waited for where the state is first used, and their
+// final-state stores need not have completed for the next item to start.
+// At the chunk's end (B3), kPending = kSideStores: a side wave issues its
+// copies at the chunk's start and its kSideStores output stores at the end,
+// and vector memory operations complete in issue order, so every copy has
+// landed while the output stores stay in flight into the next chunk.
+template <int kPending>
+__device__ __forceinline__ void split_barrier(bool chain) {
+  static_assert(kPending >= 0 && kPending < 16, "vmcnt field");
+  asm volatile("" ::: "memory");
+  if (chain)
+    __builtin_amdgcn_s_waitcnt(0xc07f);             // lgkmcnt(0)
+  else
+    __builtin_amdgcn_s_waitcnt(0x0070 | kPending);  // vmcnt(kPending), lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 struct __align__(16) SplitSmem {
   uint16_t ks[2][kChunk][kDim];
@@ -2255,19 +2279,36 @@ __device__ __forceinline__ void split_items(
     uint16_t* __restrict__ out, float* __restrict__ new_state, uint16_t* __restrict__ oi,
     float* __restrict__ slotb, uint16_t* __restrict__ slotm, int* __restrict__ mval, int4* __restrict__ fix,
     int fix_cap) {
-  const int nitems = lv.hdr[0] * 2 * kVHeads;
-  int* queue = lv.hdr + 8;
+  // The run table was written by an earlier launch and is constant here, so
+  // it is read through the constant address space: scalar loads, counted in
+  // lgkmcnt.  Vector loads would count in vmcnt behind the previous item's
+  // final-state stores, and waiting for the descriptor would wait for those.
+  const auto* runs_c = (const __attribute__((address_space(4))) u32x4*)lv.runs;
   // First items: when the groups take a whole first wave of 16 runs, the four
   // items of one (run, q/k head) (two v-heads, two halves) go to groups on the
   // same XCD (group id % 8), so the chunk's K / Q rows and both v-heads'
   // fragments are fetched into one L2.  Item (run r, q/k head hq, v-head e of
   // the pair, half) -> group 8 (4 (G / 8) + 2 e + half) + G % 8, G = 4 r + hq.
-  int first = wg;
-  if (nwg == kConsumerGroups && nitems >= kConsumerGroups) {
+  // That item's descriptor is requested together with the list header, before
+  // the run count says whether the mapping applies (one memory round trip
+  // instead of two at the kernel start).  It lies inside the run table either
+  // way: nwg is kConsumerGroups only when the table holds at least 16 runs.
+  int spec = wg;
+  if (nwg == kConsumerGroups) {
     const int x = wg & 7, slot = wg >> 3;
     const int G = 8 * (slot >> 2) + x, k = slot & 3;
-    first = 16 * (G >> 2) + 8 * (k & 1) + kGva * (G & 3) + (k >> 1);
+    spec = 16 * (G >> 2) + 8 * (k & 1) + kGva * (G & 3) + (k >> 1);
   }
+  const u32x4 spec_a = runs_c[2 * (spec >> 4)];
+  const u32x4 spec_b = runs_c[2 * (spec >> 4) + 1];
+  const int nruns = *(const __attribute__((address_space(4))) int*)lv.hdr;
+  // every value is waited for here, so the compiler cannot sink the
+  // descriptor loads below the header's wait
+  asm volatile("" ::"s"(spec_a), "s"(spec_b), "s"(nruns));
+  const int nitems = nruns * 2 * kVHeads;
+  int* queue = lv.hdr + 8;
+  const int first = nitems >= kConsumerGroups ? spec : wg;
+  bool use_spec = first == spec;
   constexpr int kFixLane = 4 * 64;   // a side-wave lane appends the M-runs' correction blocks
   // The queue and block counters are bumped by one lane.  An opaque zero
   // offset keeps the compiler from rewriting these atomics into the
@@ -2286,13 +2327,12 @@ __device__ __forceinline__ void split_items(
   };
   const int h = item & 7;
   const int hv = (item >> 3) & 1;
-  // The run table was written by an earlier launch and is constant here, so
-  // it is read through the constant address space: scalar loads, counted in
-  // lgkmcnt.  Vector loads would count in vmcnt behind the previous item's
-  // final-state stores, and waiting for the descriptor would wait for those.
-  const auto* runs_c = (const __attribute__((address_space(4))) u32x4*)lv.runs;
-  const u32x4 ua = runs_c[2 * (item >> 4)];
-  const u32x4 ub = runs_c[2 * (item >> 4) + 1];
+  u32x4 ua = spec_a, ub = spec_b;
+  if (!use_spec) {
+    ua = runs_c[2 * (item >> 4)];
+    ub = runs_c[2 * (item >> 4) + 1];
+  }
+  use_spec = false;
   const int4 ra = make_int4(static_cast<int>(ua.x), static_cast<int>(ua.y), static_cast<int>(ua.z),
                             static_cast<int>(ua.w));
   const int4 rb = make_int4(static_cast<int>(ub.x), static_cast<int>(ub.y), static_cast<int>(ub.z),
@@ -2365,7 +2405,7 @@ __device__ __forceinline__ void split_items(
     } else {
       split_dma<0>(sm, chunk_ref(0), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
     }
-    __syncthreads();
+    split_barrier<0>(chain);   // the first chunk's copies and every S fragment in place
     if (mrun && hv == 0 && tid == kFixLane) fix_pos = atomicAdd(lv.hdr + 9 + zero_v, fix_max);
     for (int i = 0; i < n; i += 2) {
       {
@@ -2379,7 +2419,7 @@ __device__ __forceinline__ void split_items(
           });
         }
         lbound += sm.gt[0][kBoundAt];
-        __syncthreads();   // B3: buffer 0 free, buffer 1 landed
+        split_barrier<kSideStores>(chain);   // B3: buffer 0 free, buffer 1 landed
       }
       if (mrun && lbound < kNegligibleLog2) {
         formed = i + 1;
@@ -2396,7 +2436,7 @@ __device__ __forceinline__ void split_items(
           });
         }
         lbound += sm.gt[1][kBoundAt];
-        __syncthreads();
+        split_barrier<kSideStores>(chain);
         if (mrun && lbound < kNegligibleLog2) {
           formed = i + 2;
           break;
