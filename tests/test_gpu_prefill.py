@@ -14,7 +14,7 @@ import torch
 
 from gpu_util import assert_parity, state_rel
 from kachua_mlsys_amd import decode, prefill
-from kachua_mlsys_amd.inputs import prefill_config, prefill_inputs_from_lengths
+from kachua_mlsys_amd.inputs import loguniform_lengths, prefill_config, prefill_inputs_from_lengths
 from oracle.gdn_oracle import decode_ref, prefill_ref
 
 pytestmark = pytest.mark.gpu
@@ -33,6 +33,18 @@ def _check(p, dev, label, **kw):
 @pytest.mark.parametrize("cfg", [2, 3, 4])
 def test_prefill_configs(gpu, cfg):
     _check(prefill_config(cfg), gpu, f"prefill c{cfg}")
+
+
+# The shapes `bench.py --reference-shapes` times against the reference's
+# published B200 figures, built the same way: one 1,377-token sequence, and
+# 8,192 tokens over 20 or 32 seeded log-uniform lengths in [128, 4096] (many
+# claimed items per consumer group, M-runs that stop early, later items that
+# load their state).
+@pytest.mark.parametrize("n", [1, 20, 32])
+def test_prefill_reference_shapes(gpu, n):
+    gen = torch.Generator("cpu").manual_seed(0)
+    lengths = [1377] if n == 1 else loguniform_lengths(n, 8192, 128, 4096, gen)
+    _check(prefill_inputs_from_lengths(lengths, gen=gen), gpu, f"reference shape N={n}")
 
 
 @pytest.mark.parametrize("lengths", [[1], [63], [64], [65], [0, 1, 63, 64, 65, 0, 130],
