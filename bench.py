@@ -6,9 +6,11 @@ Prints ONE JSON line.  The headline ``value`` is the decode step at B = 64
 (configuration 1): HBM GB/s on state traffic (state read + new_state write,
 2*64*8*128*128*4 B per step).  A "step" is one decode launch over the whole
 batch with all inputs already resident in HBM.  Timing: W untimed warmup
-steps, then exactly K steps bracketed by torch.cuda.synchronize(); the state
-buffers rotate over enough sets (> the 256 MiB Infinity Cache) that every step
-reads cold data.  The same line carries:
+steps, then exactly K steps captured in one HIP graph; the graph is replayed
+seven times, each replay bracketed by torch.cuda.synchronize() and HIP events
+on the launch stream, and the median replay sets the figure (min and max are
+reported beside it).  The state buffers rotate over enough sets (> the 256 MiB
+Infinity Cache) that every step reads cold data.  The same line carries:
 
 * ``roofline`` for the decode kernel: algorithmic bytes per launch (state +
   q, k, v, a, b, out) / mean launch duration from HIP events on the launch
@@ -42,6 +44,7 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBPS = 8000.0           # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0        # MI355X dense bf16 MFMA, published
 MALL_BYTES = 256 << 20
+DECODE_REPLAYS = 7               # timed graph replays behind the decode headline (median)
 NV, NQK, D = 8, 4, 128
 
 
@@ -84,7 +87,8 @@ def time_launches(fn, sets, steps, warmup, torch, replays=1):
     (`replays` > 1: that many timed replays, the median of their times).
 
     Returns (ms per step from HIP events on the launch stream around the replay,
-    host wall ms per step for eager launches of the same work).  The graph keeps
+    host wall ms per step for eager launches of the same work); the sorted
+    per-replay figures are left in ``time_launches.last_times``.  The graph keeps
     the ~15-20 us per-call host cost of the Python entry point out of the GPU
     timeline; the eager figure shows what a plain Python loop would get."""
     for i in range(warmup):
@@ -113,6 +117,7 @@ def time_launches(fn, sets, steps, warmup, torch, replays=1):
         torch.cuda.synchronize()
         times.append(start.elapsed_time(end) / steps)
     del graph
+    time_launches.last_times = sorted(times)
     return sorted(times)[len(times) // 2], eager_ms
 
 
@@ -230,20 +235,25 @@ def time_prefill(p_cpu, args, torch, dev, traffic=None, warm=None) -> dict:
     nsets = 1 if warm else max(2, math.ceil(2 * MALL_BYTES / per_set) + 1)
     sets = []
     for i in range(nsets):
-        q, k, v = (p.q, p.k, p.v) if i == 0 else (p.q.clone(), p.k.clone(), p.v.clone())
+        # every buffer the call reads or writes rotates (q, k, v, state, a, b,
+        # outputs, workspace), so no byte of a call is still cached from the
+        # previous call on the same set
+        def fresh(x):
+            return x if (i == 0 or x is None) else x.clone()
         o = torch.empty((T, NV, D), dtype=torch.bfloat16, device=dev)
         ns = torch.empty((N, NV, D, D), dtype=torch.float32, device=dev)
         w = ws if i == 0 else torch.empty_like(ws)
-        sets.append((q, k, v, o, ns, w))
+        sets.append((fresh(p.q), fresh(p.k), fresh(p.v), o, ns, w, fresh(p.state), fresh(p.a), fresh(p.b)))
 
     def pre_step(s):
-        prefill.launch_gdn(s[0], s[1], s[2], p.state, p.A_log, p.a, p.dt_bias, p.b,
+        prefill.launch_gdn(s[0], s[1], s[2], s[6], p.A_log, s[7], p.dt_bias, s[8],
                            p.cu_seqlens, p.scale, s[3], s[4], workspace=s[5])
 
     steps = max(10, args.steps // 4)
     # secondary figures: the median of three timed replays, so that one
     # disturbed replay does not set the number
     ev_ms, wall_ms = time_launches(pre_step, sets, steps, max(3, args.warmup // 4), torch, replays=3)
+    seg_len = planned_segment_chunks(sets[0][5], N, T, torch)
     nbytes = prefill_bytes(T, N)
     flops = prefill_flops(p.lengths)
     t_s = ev_ms * 1e-3
@@ -265,10 +275,27 @@ def time_prefill(p_cpu, args, torch, dev, traffic=None, warm=None) -> dict:
                      "tflops": round(flops / t_s / 1e12, 2),
                      "traffic": read_traffic(traffic) if traffic else None},
         "cache": "warm" if warm else f"cold ({nsets} rotated sets)",
+        "segment_chunks": seg_len,
     }
     del sets, ws
     torch.cuda.empty_cache()
     return entry
+
+
+def planned_segment_chunks(ws, N, T, torch):
+    """Segment length L (chunks) the device planner chose for the last call
+    that used workspace `ws`, or None when no sequence was split.  The list
+    header sits after the Tb fragments, the gate blocks and rec_start
+    (ws_layout in csrc/gdn_prefill.hip); header[2] is L."""
+    if T <= 2 * 64:          # the direct path: no plan
+        return None
+    def a256(x):
+        return (x + 255) // 256 * 256
+    R = -(-T // 64) + N
+    off = a256(a256(a256(R * NV * 6 * 512 * 2) + R * NV * 256 * 4) + (N + 1) * 4)
+    hdr = ws[off:off + 64].view(torch.int32).cpu().tolist()
+    L = hdr[2]
+    return L if 0 < L < (1 << 20) else None
 
 
 def chain_step_us(args, torch, dev) -> dict:
@@ -340,6 +367,35 @@ def reference_shapes(args, torch, dev) -> dict:
             "data": "synthetic (seeded randn)", "shapes": rows}
 
 
+def kernel_resources_markdown() -> str:
+    """Per-kernel resources of the HIP sources as a markdown table."""
+    import shutil
+    import subprocess
+
+    from kachua_mlsys_amd import _lib
+
+    rows = _lib.kernel_resources()
+    filt = shutil.which("c++filt") or shutil.which("llvm-cxxfilt") or "c++filt"
+
+    def demangle(name):
+        try:
+            res = subprocess.run([filt, name], capture_output=True, text=True, check=True)
+            out = res.stdout.strip()
+            return out.split("(")[0] if out else name
+        except (OSError, subprocess.CalledProcessError):
+            return name
+
+    lines = ["| kernel | source | VGPR (unified) | AGPR | SGPR | spills (v/s) | LDS B / group | scratch B "
+             "| max block | waves / SIMD (VGPR, LDS) |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        lines.append(f"| `{demangle(r['kernel'])}` | {r['source']} | {r['vgpr']} | {r['agpr']} | {r['sgpr']} | "
+                     f"{r['vgpr_spill']}/{r['sgpr_spill']} | {r['lds_bytes']} | {r['scratch_bytes']} | "
+                     f"{r['max_block']} | **{r['waves_per_simd']}** ({r['waves_per_simd_by_vgpr']}, "
+                     f"{r['waves_per_simd_by_lds']:g}) |")
+    return "\n".join(lines)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -360,7 +416,13 @@ def main():
     ap.add_argument("--reference-shapes", action="store_true",
                     help="instead of the headline line: prefill at the shapes the reference published "
                          "B200 timings for")
+    ap.add_argument("--kernel-resources", action="store_true",
+                    help="print the per-kernel resource table (registers, LDS, waves per SIMD) from the "
+                         "compiler's metadata as markdown and exit (no GPU needed)")
     args = ap.parse_args()
+    if args.kernel_resources:
+        print(kernel_resources_markdown())
+        return
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "sequences (and their states) are independent, so the decode and prefill paths "
@@ -399,11 +461,17 @@ def main():
             decode.launch_gdn(base.q, base.k, base.v, s[0], base.A_log, base.a, base.dt_bias,
                               base.b, base.scale, out, s[1])
 
-        step_ms, eager_ms = time_launches(dec_step, sets, args.steps, args.warmup, torch)
+        # median of DECODE_REPLAYS timed replays of the K-step graph; the
+        # fastest and slowest replay are reported beside it
+        step_ms, eager_ms = time_launches(dec_step, sets, args.steps, args.warmup, torch,
+                                          replays=DECODE_REPLAYS)
+        reps = time_launches.last_times
         result.update({
             "value": round(state_b / (step_ms * 1e-3) / 1e9, 1),
             "ms_per_step": round(step_ms, 5),
             "us_per_step": round(step_ms * 1e3, 3),
+            "us_per_step_replays": {"n": len(reps), "median": round(step_ms * 1e3, 3),
+                                    "min": round(reps[0] * 1e3, 3), "max": round(reps[-1] * 1e3, 3)},
             "us_per_step_eager_python_loop": round(eager_ms * 1e3, 3),
             "config": {"workload": "decode config 1: B=64, one token, fp32 state [64,8,128,128]",
                        "batch": B, "state_sets_rotated": nsets,
@@ -441,10 +509,16 @@ def main():
             if not args.warm_cache and not args.profile:
                 entry["us_per_call_warm"] = time_prefill(p_cpu, args, torch, dev, warm=True)["us_per_call"]
             if cfg in (2, 3) and step is not None:
-                # sequential floor without segment parallelism: longest sequence's chunks x step
+                # sequential floors: the longest sequence's chunks x chunk step
+                # without segments, and the longest run (at most L chunks) x
+                # step with the planner's segments (excluding the finish
+                # launch's scan and corrections)
                 nch = math.ceil(entry["max_len"] / 64)
-                entry["critical_path_floor_us"] = round(nch * step["us"], 2)
-                entry["critical_path_chunks"] = nch
+                entry["critical_path_floor_unsegmented_us"] = round(nch * step["us"], 2)
+                entry["critical_path_chunks_unsegmented"] = nch
+                run = min(nch, entry["segment_chunks"] or nch)
+                entry["critical_path_floor_segmented_us"] = round(run * step["us"], 2)
+                entry["critical_path_chunks_segmented"] = run
             if cfg == 3 and not args.no_cpu:
                 entry["cpu_baseline"] = cpu_prefill_baseline(torch, p_cpu)
             pre[f"c{cfg}"] = entry
@@ -464,6 +538,9 @@ def main():
             result["prefill_c3_us"] = pre["c3"]["us_per_call"]
             result["prefill_c3_tokens_per_s"] = pre["c3"]["tokens_per_s"]
             result["prefill_c3_roofline_frac"] = pre["c3"]["roofline"]["frac"]
+            result["prefill_c3_roofline"] = pre["c3"]["roofline"]
+            if "cpu_baseline" in pre["c3"]:
+                result["prefill_c3_cpu_baseline"] = pre["c3"]["cpu_baseline"]
 
     if args.only in ("all", "decode") and not args.no_cpu:
         result["cpu_baseline"] = cpu_decode_baseline(torch)

@@ -92,6 +92,17 @@ size_t gdn_prefill_workspace_min_bytes(int num_seqs, long long total_tokens);
  *   new_state   [num_seqs, 8, 128, 128] fp32 (written; 16-byte aligned; must not be `state`)
  *   workspace   device scratch of at least gdn_prefill_workspace_min_bytes() bytes (normally
  *               gdn_prefill_workspace_bytes()), 256-byte aligned; workspace_bytes is its size
+ *
+ * Supported input domain (outputs within allclose(atol=1e-2, rtol=1e-2) of the
+ * fp32 oracle and states within 2e-3 of its largest |state|): keys of any norm
+ * and any beta = sigmoid(b) for which every token map g (I - beta k k^T) is a
+ * contraction, i.e. |1 - beta |k|^2| <= 1 (L2-normalised keys with any b,
+ * and for example |k|^2 = 1.5 with beta <= 0.8, are tested), with any gate
+ * decay and any magnitude of v and of the state (tested from 1e-6 to 1e5, and
+ * beta down to 2e-9).  The two fp16 operands of Delta = Tb (V - gam K S^T)
+ * are scaled by powers of two into fp16's normal range before conversion.
+ * Outside that domain the recurrence itself grows without bound and the
+ * results are not specified.
  */
 int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
                     const float* A_log, const void* a, const float* dt_bias, const void* b,
@@ -112,7 +123,11 @@ int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* st
  * that the planner has fewer segment slots and results stay within tolerance.  Every call on one GPU shares that
  * GPU's array: calls that overlap in time on one GPU (other streams, other host
  * threads) race and must be ordered by the caller.  Nothing in the array needs
- * to be cleared between calls. */
+ * to be cleared between calls.  The first call on each device resolves the
+ * array's device address (which may load its code object): make that call
+ * before capturing a HIP graph on the device; later calls, captured or not,
+ * only launch kernels.  The array sits in its own code object, so processes
+ * that never call this entry point do not hold it. */
 int gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v, const float* state,
                             const float* A_log, const void* a, const float* dt_bias, const void* b,
                             const void* cu_seqlens, int cu_seqlens_is_int64, int num_seqs,

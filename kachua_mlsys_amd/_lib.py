@@ -22,7 +22,7 @@ CSRC_DIR = PKG_DIR / "csrc"
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_DIR = PKG_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libgdn_mi355x.so"
-SOURCES = ("gdn_decode.hip", "gdn_prefill.hip", "gdn_capi.hip")
+SOURCES = ("gdn_decode.hip", "gdn_prefill.hip", "gdn_noalloc.hip", "gdn_capi.hip")
 # bandwidth probe for bench.py (measurement only, not an entry point of the path)
 PROBE_PATH = LIB_DIR / "libhbm_probe.so"
 PROBE_SOURCES = ("hbm_stream.hip",)
@@ -95,6 +95,9 @@ def build_binding(verbose: bool = False) -> Path:
     from torch.utils import cpp_extension
 
     target = binding_path()
+    # a binding left from an earlier build must not outlive a failed rebuild
+    # against a newer library
+    target.unlink(missing_ok=True)
     fd, tmp = tempfile.mkstemp(prefix="_gdn_torch.", suffix=".so.tmp", dir=LIB_DIR)
     os.close(fd)
     cxx = shutil.which("c++") or shutil.which("g++")
@@ -161,8 +164,9 @@ _BINDING = None
 
 
 def load_binding():
-    """The torch binding module (built by build()); None when it is not built,
-    in which case the Python entry points validate and call the C ABI through
+    """The torch binding module (built by build()); None when it is not built
+    or was built against another ABI version than the loaded library's, in
+    which case the Python entry points validate and call the C ABI through
     ctypes themselves."""
     global _BINDING
     if _BINDING is None:
@@ -172,11 +176,11 @@ def load_binding():
         else:
             import importlib.util
 
-            load()   # the C library first: the binding resolves its symbols there
+            lib = load()   # the C library first: the binding resolves its symbols there
             spec = importlib.util.spec_from_file_location("_gdn_torch", path)
             mod = importlib.util.module_from_spec(spec)
             spec.loader.exec_module(mod)
-            _BINDING = mod
+            _BINDING = mod if getattr(mod, "ABI", None) == lib.gdn_abi_version() else False
     return _BINDING or None
 
 
@@ -201,3 +205,64 @@ def check(status: int, what: str) -> None:
     if status != 0:
         msg = load().gdn_status_string(status).decode()
         raise RuntimeError(f"{what} failed with status {status}: {msg}")
+
+
+# ---- per-kernel resource report (compiler metadata of the built sources) ----
+
+# gfx950 per-CU limits used to turn a kernel's resources into waves per SIMD
+GFX950_VGPRS_PER_LANE = 512      # unified VGPR + AGPR file of a SIMD, per lane
+GFX950_VGPR_GRANULE = 8
+GFX950_LDS_BYTES = 160 * 1024
+GFX950_MAX_WAVES_PER_SIMD = 8
+GFX950_SIMDS_PER_CU = 4
+
+
+def kernel_resources(sources=SOURCES) -> list[dict]:
+    """Per kernel of the HIP sources: VGPRs (the unified count, AGPRs
+    included), AGPRs, SGPRs, spills, LDS and scratch bytes per work-group, the
+    launch bound on the block size, and the resident waves per SIMD that
+    registers and LDS allow.  Read from the AMDGPU metadata hipcc emits for a
+    device-only assembly build of each source (the same flags as the library)."""
+    import re
+
+    rows = []
+    with tempfile.TemporaryDirectory() as td:
+        for src in sources:
+            out = Path(td) / (Path(src).stem + ".s")
+            flags = [f for f in HIPCC_FLAGS if f not in ("-shared", "-fPIC")]
+            cmd = [hipcc_path(), *flags, f"-I{INCLUDE_DIR}", "--cuda-device-only", "-S", "-o", str(out),
+                   str(CSRC_DIR / src)]
+            res = subprocess.run(cmd, capture_output=True, text=True)
+            if res.returncode != 0:
+                raise RuntimeError(f"hipcc failed on {src}:\n{res.stderr}")
+            text = out.read_text()
+            if "amdhsa.kernels:" not in text:
+                continue
+            meta = text[text.index("amdhsa.kernels:"):]
+            for blk in meta.split("\n  - ")[1:]:
+                def get(key, cast=str, default=None):
+                    m = re.search(r"(?:^|\n)\s*" + re.escape(key) + r":\s*(\S+)", blk)
+                    return cast(m.group(1)) if m else default
+                name = get(".name")
+                if name is None or name.startswith("__"):
+                    continue
+                vgpr = get(".vgpr_count", int, 0)
+                agpr = get(".agpr_count", int, 0)
+                lds = get(".group_segment_fixed_size", int, 0)
+                block = get(".max_flat_workgroup_size", int, 1024)
+                granted = -(-vgpr // GFX950_VGPR_GRANULE) * GFX950_VGPR_GRANULE
+                by_vgpr = GFX950_VGPRS_PER_LANE // max(granted, GFX950_VGPR_GRANULE)
+                waves_per_group = -(-block // 64)
+                groups_by_lds = GFX950_LDS_BYTES // lds if lds else 1 << 30
+                by_lds = groups_by_lds * waves_per_group / GFX950_SIMDS_PER_CU
+                rows.append({
+                    "source": src, "kernel": name, "vgpr": vgpr, "agpr": agpr,
+                    "sgpr": get(".sgpr_count", int, 0),
+                    "vgpr_spill": get(".vgpr_spill_count", int, 0),
+                    "sgpr_spill": get(".sgpr_spill_count", int, 0),
+                    "lds_bytes": lds, "scratch_bytes": get(".private_segment_fixed_size", int, 0),
+                    "max_block": block,
+                    "waves_per_simd": min(GFX950_MAX_WAVES_PER_SIMD, by_vgpr, int(by_lds)),
+                    "waves_per_simd_by_vgpr": by_vgpr, "waves_per_simd_by_lds": by_lds,
+                })
+    return rows

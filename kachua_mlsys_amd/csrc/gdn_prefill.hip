@@ -49,8 +49,6 @@
 // never leaves registers between chunks.
 #include "gdn_common.h"
 #include <algorithm>
-#include <atomic>
-#include <mutex>
 #include <type_traits>
 #include "../../include/gdn_mi355x.h"
 
@@ -59,10 +57,13 @@ namespace gdn {
 constexpr int kChunk = 64;
 constexpr int kFragTile = 512;               // one 16x32 MFMA operand fragment: 64 lanes x 8 16-bit values
 // Gate block per (record, v-head): gam[64], tail[64], the chunk's map bound
-// (below) at [128], Gam[64] (log2 of the cumulative gate, from which the split
-// consumer weights Aqk) at [192] (one 1 KB copy).
+// (below) at [128], the inverse of Tb's fp16 range scale (a power of two, 1
+// for Tb in fp16's usual range; see prepass_heads) at [129], Gam[64] (log2 of
+// the cumulative gate, from which the split consumer weights Aqk) at [192]
+// (one 1 KB copy).
 constexpr int kGamStride = 4 * kChunk;
 constexpr int kBoundAt = 2 * kChunk;
+constexpr int kTbScaleAt = kBoundAt + 1;
 constexpr int kLgamAt = 3 * kChunk;
 // The homogeneous part of one token's update multiplies the state by
 // g_t (I - beta_t k_t k_t^T), whose 2-norm is at most g_t max(1, |1 - beta_t |k_t|^2|).
@@ -329,6 +330,23 @@ __device__ __forceinline__ int wave_max0(int x) {
   x = max(x, dpp0<0x142, 0xa>(x));
   x = max(x, dpp0<0x143, 0xc>(x));
   return __builtin_amdgcn_readlane(x, 63);
+}
+
+// Power-of-two scale for an fp16 operand (one value per wave), from each
+// lane's maximum |x|: 1 while every |x| of the wave is below 2^15 and at
+// least one reaches 2^-4 (checked with two ballots, no cross-lane reduction);
+// otherwise the wave maximum goes to [2^10, 2^11), so the operand keeps fp16's
+// 11 significant bits at any magnitude.  Zero, inf and NaN maxima keep scale 1
+// (they pass through as in fp32).  Used for R = V - gam X (the caller divides
+// Delta = Tb R by the same power of two) and for Tb in the prepass.
+__device__ __forceinline__ float fp16_range_scale(float mx) {
+  const bool big = __builtin_amdgcn_ballot_w64(mx >= 32768.0f) != 0;
+  const bool small = __builtin_amdgcn_ballot_w64(mx >= 0.0625f) == 0;
+  if (!big && !small) return 1.0f;
+  const int bits = wave_max0(__float_as_int(mx));   // non-negative floats order as integers
+  if (bits == 0 || bits >= 0x7f800000) return 1.0f;
+  const int e = max((bits >> 23) - 127, -117);      // floor(log2 max), subnormals clamped
+  return __int_as_float((137 - e) << 23);           // 2^(10 - e)
 }
 
 // Inclusive prefix sum over the NT threads of the work-group (wave_tot: NT / 64 ints).
@@ -996,6 +1014,22 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
         if (ab >= 1) wy[ab][bb] = split_y(w[ab][bb]);
       }
     }
+    // Tb^T = diag(beta) W (row ai = 2 d + hf of fragment (m, d)).  Tb goes to
+    // fp16 scaled by a power of two that puts the wave's largest |Tb| into
+    // fp16's normal range when it is not there already (beta below about 6e-5
+    // would otherwise leave fp16 subnormals); the consumers divide Delta = Tb R
+    // by the same factor, whose inverse goes to the gate block.
+    auto tb_val = [&](int m, int ai, int rr) {
+      return (ai <= m && m < NB) ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
+    };
+    float tmx = 0.0f;
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int ai = 0; ai <= m; ++ai)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) tmx = fmaxf(tmx, fabsf(tb_val(m, ai, rr)));
+    const float tsc = fp16_range_scale(tmx);
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
 #pragma unroll
@@ -1003,16 +1037,19 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
         if (frag_zero(m, d)) continue;
         float x[8];
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          const int ai = 2 * d + hf;
+        for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = (ai <= m && m < NB) ? brow[e][ai][rr] * w[ai][m][rr] : 0.0f;
+          for (int rr = 0; rr < 4; ++rr) x[4 * hf + rr] = tb_val(m, 2 * d + hf, rr);
+        if (tsc != 1.0f) {   // uniform
+#pragma unroll
+          for (int j = 0; j < 8; ++j) x[j] *= tsc;
         }
         store_frag<kToLds>(
             u32x4{pack_h2(x[0], x[1]), pack_h2(x[2], x[3]), pack_h2(x[4], x[5]), pack_h2(x[6], x[7])},
             frag0 + e * kFragStride + (frag_slot(m, d) * 64 + lane) * 8);
       }
     }
+    if (lane == 0) gp0[e * kGamStride + kTbScaleAt] = 1.0f / tsc;   // exact: a power of two
   }
 
   // the chunk's map bound: sum over tokens of log2 g_t + log2 max(1, |1 - beta_t |k_t|^2|)
@@ -1258,25 +1295,13 @@ __device__ __forceinline__ f16x8 half_frag(const float (&x)[8]) {
                                          pack_h2(x[4], x[5]), pack_h2(x[6], x[7])});
 }
 
-// Power-of-two scale for the fp16 conversion of R = V - gam X (one value per
-// wave): 1 while every |R| of the wave is below 2^15 and at least one reaches
-// 2^-4 (checked with two ballots, no cross-lane reduction); otherwise the wave
-// maximum goes to [2^10, 2^11), so R keeps fp16's 11 significant bits at any
-// magnitude.  Zero, inf and NaN maxima keep scale 1 (they pass through as in
-// fp32).  The caller divides Delta = Tb R by the same power of two.
 __device__ __forceinline__ float r_scale(const f32x4 (&Rt)[4]) {
   float mx = 0.0f;
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) mx = fmaxf(mx, fabsf(Rt[m][rr]));
-  const bool big = __builtin_amdgcn_ballot_w64(mx >= 32768.0f) != 0;
-  const bool small = __builtin_amdgcn_ballot_w64(mx >= 0.0625f) == 0;
-  if (!big && !small) return 1.0f;
-  const int bits = wave_max0(__float_as_int(mx));   // non-negative floats order as integers
-  if (bits == 0 || bits >= 0x7f800000) return 1.0f;
-  const int e = max((bits >> 23) - 127, -117);      // floor(log2 max), subnormals clamped
-  return __int_as_float((137 - e) << 23);           // 2^(10 - e)
+  return fp16_range_scale(mx);
 }
 
 __device__ __forceinline__ bf16x8 round_frag(const float (&x)[8]) {
@@ -1509,8 +1534,9 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
       if (!frag_zero(m, d))
         D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][(frag_slot(m, d) * 64 + lane) * 8]), rf[d], D[m]);
   }
-  if (rsc != 1.0f) {
-    const float inv = 1.0f / rsc;   // exact: a power of two
+  const float tbi = sm.gt[P][kTbScaleAt];   // 1 / Tb's fp16 range scale (1 in the usual range)
+  if (rsc != 1.0f || tbi != 1.0f) {
+    const float inv = tbi / rsc;   // exact: powers of two
 #pragma unroll
     for (int m = 0; m < 4; ++m) D[m] = D[m] * inv;
   }
@@ -1996,6 +2022,7 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
   // can be waited for individually); the bound, read first, is tested after
   // the first pass.
   const float cbound = sm.gt[P][kBoundAt];   // first LDS read: done before the first K fragment
+  const float tbi = sm.gt[P][kTbScaleAt];    // 1 / Tb's fp16 range scale (1 in the usual range)
   bf16x8 ka[4][4];
   auto read_k = [&](int d) {
 #pragma unroll
@@ -2075,8 +2102,8 @@ __device__ __forceinline__ void chain_chunk(SplitSmem& sm, int c, f32x4 (&st)[8]
 #pragma unroll
     for (int m = 0; m < 4; ++m)
       if (!frag_zero(m, d)) D[m] = mfma16h(tb[d][m], rf[d], D[m]);
-  if (rsc != 1.0f) {
-    const float inv = 1.0f / rsc;   // exact: a power of two
+  if (rsc != 1.0f || tbi != 1.0f) {
+    const float inv = tbi / rsc;   // exact: powers of two
 #pragma unroll
     for (int m = 0; m < 4; ++m) D[m] = D[m] * inv;
   }
@@ -2650,7 +2677,7 @@ __device__ void state_before(FinishLds& sm, int g0, int j, int h, const float* _
   }
 }
 
-__global__ __launch_bounds__(kFinThreads) void finish_kernel(int* __restrict__ lists, int num_seqs, int gcap,
+__global__ __launch_bounds__(kFinThreads, 2) void finish_kernel(int* __restrict__ lists, int num_seqs, int gcap,
                                                              const int4* __restrict__ fix, int fix_cap,
                                                              const float* __restrict__ slotb,
                                                              const uint16_t* __restrict__ slotm,
@@ -2779,7 +2806,7 @@ namespace gdn {
 
 // The prefill launches for a workspace of workspace_bytes bytes (both entry
 // points below): argument checks first, nothing launched on a rejection.
-static int prefill_launch(const void* q, const void* k, const void* v, const float* state,
+int prefill_launch(const void* q, const void* k, const void* v, const float* state,
                           const float* A_log, const void* a, const float* dt_bias,
                           const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
                           int num_seqs, long long total_tokens, float scale, void* output,
@@ -2888,41 +2915,6 @@ static int prefill_launch(const void* q, const void* k, const void* v, const flo
   return err == hipSuccess ? GDN_OK : static_cast<int>(err);
 }
 
-// ---- no-allocation variant: the workspace is a file-scope device array ----
-// Each GPU the library runs on holds one copy until the process ends.  Host
-// code never passes the array's name to a kernel (on the host it is only a
-// stand-in for the symbol): the device address comes from hipGetSymbolAddress,
-// taken once per device with that device current, on the entry point's first
-// call there.
-static_assert(GDN_PREFILL_NOALLOC_SCRATCH_BYTES % 256 == 0, "scratch size");
-static __device__ __align__(256) unsigned char scratch[GDN_PREFILL_NOALLOC_SCRATCH_BYTES];
-
-constexpr int kMaxDevices = 64;
-static std::atomic<void*> g_scratch_ptr[kMaxDevices];
-static std::mutex g_scratch_mu;
-
-// Device address of the current device's scratch array (its first call on a
-// device resolves the symbol).  Returns GDN_OK or an error code.
-static int current_scratch(void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return static_cast<int>(e);
-  if (dev < 0 || dev >= kMaxDevices) return GDN_ERR_INVALID_ARGUMENT;
-  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
-  if (p == nullptr) {
-    std::lock_guard<std::mutex> lock(g_scratch_mu);
-    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
-    if (p == nullptr) {
-      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-      if (e != hipSuccess) return static_cast<int>(e);
-      if (p == nullptr) return GDN_ERR_INVALID_ARGUMENT;
-      g_scratch_ptr[dev].store(p, std::memory_order_release);
-    }
-  }
-  *out = p;
-  return GDN_OK;
-}
-
 }  // namespace gdn
 
 extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, const float* state,
@@ -2933,25 +2925,4 @@ extern "C" int gdn_prefill_fwd(const void* q, const void* k, const void* v, cons
                                void* stream) {
   return gdn::prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64, num_seqs,
                              total_tokens, scale, output, new_state, workspace, workspace_bytes, stream);
-}
-
-extern "C" int gdn_prefill_fwd_noalloc(const void* q, const void* k, const void* v, const float* state,
-                                       const float* A_log, const void* a, const float* dt_bias,
-                                       const void* b, const void* cu_seqlens, int cu_seqlens_is_int64,
-                                       int num_seqs, long long total_tokens, float scale, void* output,
-                                       float* new_state, void* stream) {
-  using namespace gdn;
-  if (num_seqs < 0 || total_tokens < 0) return GDN_ERR_INVALID_ARGUMENT;
-  if (num_seqs == 0) return GDN_OK;
-  if (gdn_prefill_workspace_min_bytes(num_seqs, total_tokens) > GDN_PREFILL_NOALLOC_SCRATCH_BYTES)
-    return GDN_ERR_TOO_LARGE;
-  void* ws = nullptr;
-  const int st = current_scratch(&ws);
-  if (st != GDN_OK) return st;
-  // the default workspace's slot count when it fits, so results equal
-  // gdn_prefill_fwd's with a default workspace
-  const size_t bytes = std::min<size_t>(GDN_PREFILL_NOALLOC_SCRATCH_BYTES,
-                                        gdn_prefill_workspace_bytes(num_seqs, total_tokens));
-  return prefill_launch(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_is_int64, num_seqs,
-                        total_tokens, scale, output, new_state, ws, bytes, stream);
 }

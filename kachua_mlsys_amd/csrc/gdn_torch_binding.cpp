@@ -97,6 +97,9 @@ int prefill(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v, const
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.attr("NOT_FAST") = kNotFast;
+  // the C ABI this binding was compiled against (gdn_mi355x.h); the loader
+  // refuses the binding when the library reports another version
+  m.attr("ABI") = GDN_ABI_VERSION;
   m.def("decode", &decode);
   m.def("prefill", &prefill);
 }

@@ -6,10 +6,14 @@ Loaded by path, like the reference harness loads its entry modules
 function is also registered as "flashinfer.kernel", as the reference does.
 """
 
+import os
 import sys
 from pathlib import Path
 
-_REPO = Path(__file__).resolve().parents[3]
+# The repository root: KACHUA_MLSYS_AMD_ROOT when set (a copy of this file
+# placed in the reference's solution/triton/ directory), else the checkout
+# this file sits in.
+_REPO = Path(os.environ.get("KACHUA_MLSYS_AMD_ROOT") or Path(__file__).resolve().parents[3])
 if str(_REPO) not in sys.path:
     sys.path.insert(0, str(_REPO))
 

@@ -179,6 +179,61 @@ def test_solution_dirs_point_at_entry_points(definition, module):
     assert getattr(mod, fn) is module.launch_gdn
 
 
+# The reference harness's loader rules, restated:
+# * gdn_prefill_qk4_v8_d128_k_last/scripts/bench_fi_timing.py:85-108 accepts
+#   only build.language == "triton", splits entry_point on "::", loads the file
+#   by path under the module name "triton_kernel" and calls the function with
+#   12 positional arguments (q, k, v, state, A_log, a, dt_bias, b, cu_seqlens,
+#   scale, out, new_state);
+# * the contest packer maps a plain Python entry module to BuildSpec language
+#   "triton" (gdn_decode_qk4_v8_d128_k_last/scripts/run_modal.py:91-97);
+# * the decode timing script's binding calls launch_gdn with 11 positional
+#   arguments (gdn_decode_qk4_v8_d128_k_last/scripts/bench_fi_timing.py:98-114).
+@pytest.mark.parametrize("definition,nargs", [("gdn_decode_qk4_v8_d128_k_last", 11),
+                                              ("gdn_prefill_qk4_v8_d128_k_last", 12)])
+def test_solution_dirs_pass_reference_loader_rules(definition, nargs):
+    import inspect
+
+    import tomli
+    sol = REPO / "kachua_mlsys_amd" / "solutions" / definition
+    cfg = tomli.loads((sol / "config.toml").read_text())
+    assert cfg["build"]["language"] == "triton"
+    assert cfg["build"].get("binding") is None
+    entry_file, fn = cfg["build"]["entry_point"].split("::", maxsplit=1)
+    assert entry_file == "kernel.py" and fn == "launch_gdn"
+    spec = importlib.util.spec_from_file_location("triton_kernel", str(sol / entry_file))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    sig = inspect.signature(getattr(mod, fn))
+    sig.bind(*range(nargs))                     # the harness's positional call binds
+    with pytest.raises(TypeError):
+        sig.bind(*range(nargs + 1))
+
+
+def test_entry_module_copied_into_reference_layout(tmp_path):
+    # a copy of the prefill entry module at <project>/solution/triton/kernel.py
+    # (where the reference's prefill script looks) finds this checkout through
+    # KACHUA_MLSYS_AMD_ROOT
+    import os
+    import shutil
+    import subprocess
+    import sys
+
+    dst = tmp_path / "solution" / "triton"
+    dst.mkdir(parents=True)
+    shutil.copy(REPO / "kachua_mlsys_amd" / "solutions" / "gdn_prefill_qk4_v8_d128_k_last" / "kernel.py",
+                dst / "kernel.py")
+    code = ("import importlib.util, sys\n"
+            f"spec = importlib.util.spec_from_file_location('triton_kernel', {str(dst / 'kernel.py')!r})\n"
+            "mod = importlib.util.module_from_spec(spec); spec.loader.exec_module(mod)\n"
+            "print(mod.launch_gdn.__module__)\n")
+    env = dict(os.environ, KACHUA_MLSYS_AMD_ROOT=str(REPO), PYTHONPATH="")
+    res = subprocess.run([sys.executable, "-c", code], cwd=tmp_path, env=env, capture_output=True, text=True,
+                         timeout=300)
+    assert res.returncode == 0, res.stderr
+    assert res.stdout.strip() == "kachua_mlsys_amd.prefill"
+
+
 def test_c_prefill_noalloc_rejects_before_launch(lib):
     # the no-allocation entry point: rejected sizes and arguments launch nothing
     f = lib.gdn_prefill_fwd_noalloc

@@ -339,3 +339,41 @@ def test_prefill_torch_binding_path(gpu):
     assert torch.equal(o2.view(torch.int16), o3.view(torch.int16)) and torch.equal(s2, s3)
     with pytest.raises(ValueError, match="alias"):
         prefill.launch_gdn(*p.to(gpu).args()[:3], ns, *g.args()[4:], out, ns)
+
+
+# Key / write-strength domain beyond the benchmark distribution.  The oracle
+# (reference_torch_impl.py:66-88) neither normalises keys nor bounds beta.
+# * Un-normalised keys where every token map g (I - beta k k^T) is still a
+#   contraction: |k|^2 = 1.5 with beta <= 0.8 (|1 - beta |k|^2| <= 1), with
+#   the default and with near-1 decay.
+# * Tiny beta (b = -14: beta = 8.3e-7; b = -20: 2.1e-9): Tb = (I + N)^-1
+#   diag(beta) would fall into fp16 subnormals (a CPU emulation of the
+#   kernel's roundings gives state errors 1.3e-2 and 1.0 without the prepass's
+#   power-of-two range scale of Tb, 2.4e-4 and 4.4e-4 with it).  A zero initial
+#   state makes the whole state come from those small writes; a random one
+#   decays away under the default gates.  Direct, short and segmented paths.
+def _scaled_keys(p, norm2):
+    k = p.k.float()
+    p.k = (k / k.norm(dim=-1, keepdim=True) * norm2 ** 0.5).to(torch.bfloat16)
+    return p
+
+
+@pytest.mark.parametrize("lengths,weak", [([1000, 64, 2000, 5], False), ([1000, 64, 2000, 5], True),
+                                           ([100, 20], False)])
+def test_prefill_unnormalised_keys(gpu, lengths, weak):
+    p = _scaled_keys(prefill_inputs_from_lengths(lengths, seed=sum(lengths) % 89), 1.5)
+    p.b = p.b.float().clamp(max=1.38).to(torch.bfloat16)    # beta <= sigmoid(1.38) < 0.8
+    if weak:
+        p.A_log = torch.linspace(-8.0, -5.0, 8)
+    _check(p, gpu, f"|k|^2 = 1.5, beta <= 0.8, weak={weak}, lengths={lengths}")
+
+
+@pytest.mark.parametrize("b_val", [-14.0, -20.0])
+@pytest.mark.parametrize("lengths,state_none", [([100, 20], True), ([1000, 64, 40, 2000], True),
+                                                 ([1000, 64, 40, 2000], False), ([30] * 70, True)])
+def test_prefill_tiny_beta(gpu, b_val, lengths, state_none):
+    p = prefill_inputs_from_lengths(lengths, seed=len(lengths) + 17)
+    p.b = torch.full_like(p.b, b_val)
+    if state_none:
+        p.state = None
+    _check(p, gpu, f"beta = sigmoid({b_val}), state_none={state_none}, lengths={lengths[:6]}")

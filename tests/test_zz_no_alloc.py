@@ -1,7 +1,8 @@
-"""GPU test of gdn_prefill_fwd_noalloc (workspace from the library's static
+"""GPU tests of gdn_prefill_fwd_noalloc (workspace from the library's static
 device array) through the C ABI: two calls in a row, the second on a smaller
 batch, each bit-identical to gdn_prefill_fwd with a default workspace and within
-the oracle tolerance."""
+the oracle tolerance; and the call captured into a HIP graph after one eager
+call on the device, every replay bit-identical to the eager result."""
 
 import ctypes
 
@@ -48,3 +49,40 @@ def test_prefill_noalloc_two_calls(gpu, run):
         assert torch.equal(ns, ref_ns), "new_state differs from gdn_prefill_fwd"
         o_ref, s_ref, o32 = prefill_ref(*p.args(), return_fp32_out=True)
         assert_parity(out, ns, o32, s_ref, f"noalloc {lengths}")
+
+
+def test_prefill_noalloc_graph_capture(gpu):
+    # The first call on a device resolves the array's address (which can load
+    # its code object), so it is made eagerly; the captured call then records
+    # kernels only, and replays with other eager work in between match.
+    lib = _lib.load()
+    lengths = [900, 64, 1300, 0, 33]
+    print(f"[case] noalloc graph capture lengths={lengths}", flush=True)
+    p = prefill_inputs_from_lengths(lengths, seed=63)
+    T, N = p.q.shape[0], len(lengths)
+    g = p.to(gpu)
+    ref_out = torch.empty((T, 8, 128), dtype=torch.bfloat16, device=gpu)
+    ref_ns = torch.empty((N, 8, 128, 128), device=gpu)
+    st = _noalloc(lib, g, ref_out, ref_ns)
+    assert st == 0, lib.gdn_status_string(st)
+    torch.cuda.synchronize()
+    out = torch.empty_like(ref_out)
+    ns = torch.empty_like(ref_ns)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st = _noalloc(lib, g, out, ns)
+    assert st == 0, lib.gdn_status_string(st)
+    other = prefill_inputs_from_lengths([300, 5, 70], seed=5).to(gpu)
+    oo = torch.empty((other.q.shape[0], 8, 128), dtype=torch.bfloat16, device=gpu)
+    on = torch.empty((3, 8, 128, 128), device=gpu)
+    for r in range(3):
+        out.fill_(7.0)
+        ns.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16)), f"replay {r}: output differs"
+        assert torch.equal(ns, ref_ns), f"replay {r}: new_state differs"
+        # eager work between replays, through the same device array
+        assert _noalloc(lib, other, oo, on) == 0
+        torch.cuda.synchronize()
+    del graph
