@@ -451,6 +451,7 @@ constexpr int kPlanScratch = kPsMisc + 4;
 // not known).
 template <int NT>
 __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, long long T, int R, int gcap,
+                          const float* __restrict__ A_log, const float* __restrict__ dt_bias,
                           int* __restrict__ rec_start, int* __restrict__ lists, int* ps, int& total_recs,
                           long long t0_first = 0, long long t1_first = -1) {
   constexpr int kW = NT / 64;
@@ -527,6 +528,11 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
   for (int i = tid; i < 2 * kBuckets; i += NT) ps[kPsHist + i] = 0;
   __syncthreads();
   if (wv == 0) {
+    // fraction of v-heads that decay slowly (see below), lanes 0-7 one head each
+    const bool slow_h = lane < kVHeads &&
+                        2.0f * kChunk * kLog2e * log_decay(A_log[min(lane, kVHeads - 1)], 0.0f,
+                                                           dt_bias[min(lane, kVHeads - 1)]) > kNegligibleLog2;
+    const float slow_frac = static_cast<float>(__popcll(__builtin_amdgcn_ballot_w64(slow_h))) / kVHeads;
     // lane i < kSegCands evaluates candidate i, in chunk steps of the split
     // consumer: the longest run and the average work-group load (chunk runs
     // plus a per-item overhead) bound the critical path; the scan adds half a
@@ -549,7 +555,22 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
     const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
     const int nseg_max = ml > 0 ? (ml - 1) / Lc + 1 : 0;
-    const float est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    float est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    // Slowly decaying heads: their segment maps never become negligible, so
+    // every correction block of segment j >= 2 in the finish first takes j - 1
+    // scan steps.  The heads' chunk map bound is estimated from the per-head
+    // constants (a = 0): 64 log2 g = -64 log2(e) exp(A_log) softplus(dt_bias);
+    // a head is slow when two chunks do not reach the negligible bound.  Such
+    // batches pay about kScanStepCost chunk steps per chunk of the longest
+    // sequence's segments j >= 2, weighted by j - 1 (measured with forced
+    // segment lengths on configuration 3 with near-1 decay).
+    if (slow_frac > 0.f && nseg_max >= 3) {
+      constexpr float kScanStepCost = 0.45f;
+      const int last = ml - (nseg_max - 1) * Lc;
+      const float pj = static_cast<float>(Lc) * static_cast<float>((nseg_max - 3) * (nseg_max - 2) / 2) +
+                       static_cast<float>(last) * static_cast<float>(nseg_max - 2);
+      est += slow_frac * kScanStepCost * pj;
+    }
     // key: estimate in 1/16 steps, then the longer candidate; invalid lanes hold the maximum
     const int q = static_cast<int>(fminf(est * 16.f, 1.0e7f));
     const int key = (lane < kSegCands && slots <= gcap) ? q * 64 + (63 - lane) : 0x7fffffff;
@@ -673,6 +694,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
 // table the prepass reads.
 __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
     const void* __restrict__ cu, int is64, int num_seqs, long long T, int R, int gcap,
+    const float* __restrict__ A_log, const float* __restrict__ dt_bias,
     int* __restrict__ rec_start, int4* __restrict__ recs, int* __restrict__ lists) {
   __shared__ int ps[kPlanScratch];
   const int tid = threadIdx.x;
@@ -680,7 +702,8 @@ __global__ __launch_bounds__(kPlanThreads) void plan_kernel(
   const int s_begin = min(tid * per, num_seqs);
   const int s_end = min(num_seqs, s_begin + per);
   int total_recs;
-  int base = plan_batch<kPlanThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, ps, total_recs);
+  int base = plan_batch<kPlanThreads>(cu, is64, num_seqs, T, R, gcap, A_log, dt_bias, rec_start, lists, ps,
+                                      total_recs);
   for (int s = s_begin; s < s_end; ++s) {
     long long t0, t1;
     seq_bounds(cu, is64, s, T, t0, t1);
@@ -1115,7 +1138,8 @@ __global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
     // work-group 0 plans the batch (lists for the consumer) while the others
     // run the records
     int total_recs;
-    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, rec_start, lists, sm.u.plan, total_recs);
+    plan_batch<kPrepassThreads>(cu, is64, num_seqs, T, R, gcap, A_log, dt_bias, rec_start, lists, sm.u.plan,
+                                total_recs);
     return;
   }
   const int lane = threadIdx.x & 63;
@@ -2873,7 +2897,8 @@ int prefill_launch(const void* q, const void* k, const void* v, const float* sta
   const int fused_plan = num_seqs <= kFusedPlanSeqs ? 1 : 0;
   if (!fused_plan)
     plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, st>>>(cu_seqlens, cu_seqlens_is_int64, num_seqs,
-                                                        total_tokens, Ri, gc, rec_start, recs, lists);
+                                                        total_tokens, Ri, gc, A_log, dt_bias, rec_start, recs,
+                                                        lists);
   // one wave per (record, v-head) while every item fits in one round: two
   // waves per SIMD for up to 2048 items (a lone item's latency matters there),
   // three (a tighter register budget) for up to 3072.  Larger batches take one
