@@ -125,6 +125,7 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 // in one entry, so an item costs one dependent load before its data.
 //   hdr[0] runs, [1] short sequences, [2] segment length L (chunks),
 //   [3] multi-segment sequences, [4] segments >= 1 over all sequences,
+//   [5] 1 when the batch uses warm-up segments (no M-runs, no finish work),
 //   [8] split-consumer work queue (items claimed past each group's first),
 //   [9] correction blocks appended by the consumer's M-runs
 //   multi[e]   = (seq, first slot, segments, 0)
@@ -134,13 +135,29 @@ __host__ __device__ inline long long max_segments(long long tokens) {
 //   runs[2i]   = (seq, flags | tokens of the run's last chunk << 8 | segment
 //                 j << 16, final-state slot or -1 for new_state, first record)
 //   runs[2i+1] = (first token lo, hi, chunks with records, chunks)
-//   flags: kRunM (M-run), kRunFromState (initial state from `state`)
+//   flags: kRunM (M-run), kRunFromState (initial state from `state`),
+//          kRunWarm (warm-up run, below); final-state slot -1: new_state,
+//          -2: none (a warm-up run of a segment before the last)
 //   shorts[i]  = (seq, record of its chunk or -1 when it has none, first token
 //                 lo, first token hi | tokens << 16) for sequences of at most
 //                 one chunk
 constexpr int kListHdr = 16;
 constexpr int kRunM = 1;
 constexpr int kRunFromState = 2;
+constexpr int kRunWarm = 4;
+// Warm-up segments.  When every v-head's segment map becomes negligible within
+// a few chunks, segment j >= 1 needs no M-run and no correction: its run starts
+// W chunks before the segment, from a zero state, with W the fewest preceding
+// chunks whose map bounds sum below kNegligibleLog2.  The state it carries
+// into the segment then differs from the true one by less than 2^-30 of the
+// state those chunks started from (the criterion an M-run stops on), and it
+// discards the outputs of the warm-up chunks.  The run finds W itself from the
+// prepass's chunk bounds; if they never get that low it starts at the
+// sequence's first chunk from the true initial state, which is exact.  The
+// planner takes this scheme when its estimate of every head's warm-up (from
+// A_log and dt_bias) is at most kWarmMaxChunks.
+constexpr int kWarmMaxChunks = 4;
+constexpr int kSlotNone = -2;
 
 // Finish work: a correction block is one or more chunks of one (segment,
 // v-head); wave w of a finish group corrects 16-token tile w of each chunk.
@@ -411,16 +428,22 @@ struct SeqPlan {
   int is_long, nseg, multi, full_seg, full_runs, part_runs, last;
 };
 
-__device__ __forceinline__ SeqPlan seq_plan(int nch, int L) {
+__device__ __forceinline__ SeqPlan seq_plan(int nch, int L, bool warm) {
   SeqPlan p = {0, 0, 0, 0, 0, 0, 0};
   if (nch < kLongChunks) return p;
   p.is_long = 1;
   p.nseg = (nch - 1) / L + 1;
-  p.multi = p.nseg >= 2 ? 1 : 0;
   p.last = nch - (p.nseg - 1) * L;
   p.full_seg = p.last == L ? p.nseg : p.nseg - 1;
-  p.full_runs = p.full_seg > 0 ? 2 * p.full_seg - 1 : 0;
-  p.part_runs = p.last == L ? 0 : (p.nseg == 1 ? 1 : 2);
+  if (warm) {   // one run per segment, no M-runs, nothing for the finish
+    p.multi = 0;
+    p.full_runs = p.full_seg;
+    p.part_runs = p.last == L ? 0 : 1;
+  } else {
+    p.multi = p.nseg >= 2 ? 1 : 0;
+    p.full_runs = p.full_seg > 0 ? 2 * p.full_seg - 1 : 0;
+    p.part_runs = p.last == L ? 0 : (p.nseg == 1 ? 1 : 2);
+  }
   return p;
 }
 
@@ -528,17 +551,25 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
   for (int i = tid; i < 2 * kBuckets; i += NT) ps[kPsHist + i] = 0;
   __syncthreads();
   if (wv == 0) {
-    // fraction of v-heads that decay slowly (see below), lanes 0-7 one head each
-    const bool slow_h = lane < kVHeads &&
-                        2.0f * kChunk * kLog2e * log_decay(A_log[min(lane, kVHeads - 1)], 0.0f,
-                                                           dt_bias[min(lane, kVHeads - 1)]) > kNegligibleLog2;
+    // per v-head (lanes 0-7) the log2 bound of one chunk's map, estimated from
+    // the per-head constants (a = 0): 64 log2 g = -64 log2(e) exp(A_log) softplus(dt_bias)
+    const float hb = lane < kVHeads
+                         ? kChunk * kLog2e * log_decay(A_log[min(lane, kVHeads - 1)], 0.0f,
+                                                       dt_bias[min(lane, kVHeads - 1)])
+                         : -1.0e30f;
+    // fraction of v-heads that decay slowly (see below)
+    const bool slow_h = lane < kVHeads && 2.0f * hb > kNegligibleLog2;
     const float slow_frac = static_cast<float>(__popcll(__builtin_amdgcn_ballot_w64(slow_h))) / kVHeads;
+    // warm-up chunks each head needs (estimate), and the scheme
+    const int wh = hb < kNegligibleLog2 ? 1 : (hb < 0.f ? static_cast<int>(ceilf(kNegligibleLog2 / hb)) : 1 << 20);
+    const int w_est = wave_max0(min(wh, 1 << 20));
+    const bool warm = w_est <= kWarmMaxChunks;
     // lane i < kSegCands evaluates candidate i, in chunk steps of the split
     // consumer: the longest run and the average work-group load (chunk runs
     // plus a per-item overhead) bound the critical path; the scan adds half a
     // step per segment and segmenting at all 1.5 steps.  The minimum over the
     // lanes wins, ties to the longer segments.
-    float sl = 0.f, a = 0.f, runs = 0.f;
+    float sl = 0.f, a = 0.f, runs = 0.f, nlong = 0.f;
     long long slots = 0;
     int ml = 0;
     const int ci = min(lane, kSegCands - 1);
@@ -549,13 +580,30 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       a += static_cast<float>(pj[ci]);
       slots += pj[kSegCands + ci];
       runs += static_cast<float>(pj[2 * kSegCands + ci]);
+      nlong += static_cast<float>(pj[2 * kSegCands + kSegCands - 1]);   // the no-split candidate: one run each
     }
     constexpr float kItemOverhead = 1.0f;   // chunk steps per work item (metadata, state, first copies)
     const int Lc = seg_cand(ci);
-    const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
-    const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
     const int nseg_max = ml > 0 ? (ml - 1) / Lc + 1 : 0;
-    float est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    float est;
+    if (warm) {
+      // one run per segment (runs = sum of 2 nseg - 1 -> sum of nseg), each
+      // later segment w_est chunks longer; nothing for the finish
+      const float runs_w = 0.5f * (runs + nlong);
+      const float later = runs_w - nlong;
+      const float per_wg =
+          (16.f * (sl + static_cast<float>(w_est) * later) + kItemOverhead * 16.f * runs_w) / kConsumerGroups;
+      const float crit =
+          static_cast<float>(min(Lc, ml) + (nseg_max > 1 ? w_est : 0)) + kItemOverhead;
+      est = fmaxf(crit, per_wg);
+      // No slot is written in this scheme, but the slot bound still applies:
+      // the run table holds max_runs(N, gcap) = N + 2 gcap runs, and with at
+      // most gcap later segments the runs (one per segment) stay within it.
+    } else {
+      const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
+      const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
+      est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    }
     // Slowly decaying heads: their segment maps never become negligible, so
     // every correction block of segment j >= 2 in the finish first takes j - 1
     // scan steps.  The heads' chunk map bound is estimated from the per-head
@@ -564,7 +612,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     // batches pay about kScanStepCost chunk steps per chunk of the longest
     // sequence's segments j >= 2, weighted by j - 1 (measured with forced
     // segment lengths on configuration 3 with near-1 decay).
-    if (slow_frac > 0.f && nseg_max >= 3) {
+    if (!warm && slow_frac > 0.f && nseg_max >= 3) {
       constexpr float kScanStepCost = 0.45f;
       const int last = ml - (nseg_max - 1) * Lc;
       const float pj = static_cast<float>(Lc) * static_cast<float>((nseg_max - 3) * (nseg_max - 2) / 2) +
@@ -576,17 +624,21 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     const int key = (lane < kSegCands && slots <= gcap) ? q * 64 + (63 - lane) : 0x7fffffff;
     // minimum over the lanes: the maximum of the complements
     const int best = 0x7fffffff - wave_max0(0x7fffffff - key);
-    if (lane == 0) ps[kPsMisc] = seg_cand(63 - (best & 63));
+    if (lane == 0) {
+      ps[kPsMisc] = seg_cand(63 - (best & 63));
+      ps[kPsMisc + 1] = warm ? 1 : 0;
+    }
   }
   __syncthreads();
   const int L = ps[kPsMisc];
+  const bool warm = ps[kPsMisc + 1] != 0;
 
   // ---- pass 2: per-sequence counts and their prefix sums ----
   // v: records, short sequences, multi-segment sequences, slots, full runs
   int v[5] = {0, 0, 0, 0, 0};
   for (int s = s_begin; s < s_end; ++s) {
     const int nch = chunks(s);
-    const SeqPlan p = seq_plan(nch, L);
+    const SeqPlan p = seq_plan(nch, L, warm);
     v[0] += nch;
     v[1] += p.is_long ? 0 : 1;
     v[2] += p.multi;
@@ -622,6 +674,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       lv.hdr[2] = L;
       lv.hdr[3] = tot[2];
       lv.hdr[4] = tot[3] - tot[2];
+      lv.hdr[5] = warm ? 1 : 0;
       rec_start[num_seqs] = min(tot[0], R);
     }
   }
@@ -635,7 +688,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     long long t0, t1;
     bounds(s, t0, t1);
     const int nch = static_cast<int>((t1 - t0 + kChunk - 1) / kChunk);
-    const SeqPlan p = seq_plan(nch, L);
+    const SeqPlan p = seq_plan(nch, L, warm);
     const int rec0 = rb;
     rec_start[s] = rb;
     rb += nch;
@@ -670,15 +723,15 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       const long long rfirst = rec0 + i0;
       // chunks whose records exist (overlapping cu_seqlens can exhaust the capacity)
       const int nvalid = static_cast<int>(max(0LL, min(static_cast<long long>(nrun), R - rfirst)));
-      const int flags = (mrun ? kRunM : 0) | (!mrun && j == 0 ? kRunFromState : 0);
-      const int slot = p.multi ? g0 + j : -1;
+      const int flags = (mrun ? kRunM : 0) | (!mrun && j == 0 ? kRunFromState : 0) | (warm && j > 0 ? kRunWarm : 0);
+      const int slot = p.multi ? g0 + j : (warm && j < p.nseg - 1 ? kSlotNone : -1);
       lv.runs[2 * pos] = make_int4(s, flags | (last_tok << 8) | (j << 16), slot,
                                    static_cast<int>(min(rfirst, 0x7fffffffLL)));
       lv.runs[2 * pos + 1] = make_int4(static_cast<int>(c0 & 0xffffffffLL), static_cast<int>(c0 >> 32), nvalid, nrun);
     };
     for (int j = 0; j < p.full_seg; ++j) {
       emit_run(fp++, j, false);
-      if (j > 0) emit_run(fp++, j, true);
+      if (j > 0 && !warm) emit_run(fp++, j, true);
     }
     if (p.part_runs) {
       const int pos = atomicAdd(&ps[kPsCur + len_bucket(p.last)], p.part_runs);
@@ -2352,10 +2405,13 @@ __device__ __forceinline__ void split_items(
   }
   const u32x4 spec_a = runs_c[2 * (spec >> 4)];
   const u32x4 spec_b = runs_c[2 * (spec >> 4) + 1];
-  const int nruns = *(const __attribute__((address_space(4))) int*)lv.hdr;
+  const auto* hdr_c = (const __attribute__((address_space(4))) int*)lv.hdr;
+  const int nruns = hdr_c[0];
+  const int seg_len = hdr_c[2];
   // every value is waited for here, so the compiler cannot sink the
   // descriptor loads below the header's wait
-  asm volatile("" ::"s"(spec_a), "s"(spec_b), "s"(nruns));
+  asm volatile("" ::"s"(spec_a), "s"(spec_b), "s"(nruns), "s"(seg_len));
+  const auto* gam_c = (const __attribute__((address_space(4))) float*)ws_gam;
   const int nitems = nruns * 2 * kVHeads;
   int* queue = lv.hdr + 8;
   const int first = nitems >= kConsumerGroups ? spec : wg;
@@ -2390,11 +2446,38 @@ __device__ __forceinline__ void split_items(
                             static_cast<int>(ub.w));
   const int s = ra.x, slot = ra.z, rfirst = ra.w;
   const bool mrun = (ra.y & kRunM) != 0;
-  const bool from_state = (ra.y & kRunFromState) != 0;
+  bool from_state = (ra.y & kRunFromState) != 0;
   const int last_tok = min((ra.y >> 8) & 0xff, kChunk);   // the chunk length indexes 64-entry LDS rows
   const int jseg = ra.y >> 16;
   const long long c0r = static_cast<long long>(static_cast<unsigned>(rb.x)) | (static_cast<long long>(rb.y) << 32);
-  const int n = rb.z, nrun = rb.w;
+  const int nrun = rb.w;
+  // A warm-up run (kRunWarm) starts `warmup` chunks before its segment: the
+  // fewest preceding chunks of the sequence whose map bounds (gate block,
+  // written by the prepass) sum below kNegligibleLog2, read newest first, four
+  // per round trip; when even all of them do not, it starts at the sequence's
+  // first chunk from the initial state.  Every wave computes the same value.
+  int warmup = 0;
+  if ((ra.y & kRunWarm) != 0 && rb.z > 0) {
+    const int before = jseg * seg_len;   // chunks of the sequence before the segment
+    float acc = 0.0f;
+    while (warmup < before && acc >= kNegligibleLog2) {
+      float b4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int back = min(warmup + q + 1, before);
+        b4[q] = gam_c[(static_cast<size_t>(rfirst - back) * kVHeads + h) * kGamStride + kBoundAt];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if (warmup < before && acc >= kNegligibleLog2) {
+          acc += b4[q];
+          ++warmup;
+        }
+      }
+    }
+    if (acc >= kNegligibleLog2) from_state = true;   // warmup == before: the sequence's initial state
+  }
+  const int n = rb.z + warmup;   // chunks this item runs, warm-up chunks first
   const int hq = h / kGva;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -2403,7 +2486,9 @@ __device__ __forceinline__ void split_items(
   const int lane = tid & 63;
   const int l16 = lane & 15, lg = lane >> 4;
   const int vcol = kHalfV * hv + 16 * wt;
-  auto chunk_ref = [&](int li) {
+  // chunk i of the item is chunk i - warmup of the run (negative: warm-up chunks, all full)
+  auto chunk_ref = [&](int i) {
+    const int li = i - warmup;
     return ChunkRef{c0r + static_cast<long long>(li) * kChunk, li == nrun - 1 ? last_tok : kChunk, rfirst + li};
   };
   auto kappa = [&](int kt, int rr) { return 32 * (kt >> 1) + 8 * lg + 4 * (kt & 1) + rr; };
@@ -2425,9 +2510,10 @@ __device__ __forceinline__ void split_items(
   }
   uint16_t* obase = mrun ? oi : out;
   const uint32_t ocol = 2u * static_cast<uint32_t>(vcol + 4 * lg);
-  auto out_rsrc = [&](const ChunkRef& cr) {
+  // output rows of chunk i: none for warm-up chunks (the stores fall outside the resource)
+  auto out_rsrc = [&](int i, const ChunkRef& cr) {
     return buf_rsrc(obase + (static_cast<size_t>(cr.c0) * kVHeads + h) * kDim,
-                    static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
+                    i < warmup ? 0u : static_cast<uint32_t>(cr.c) * (kVHeads * kDim * 2));
   };
   const SplitDmaLane dl = split_dma_lane(wt, lane, hv);
   // Correction blocks of the segment: chunks [0, formed) get O0 + OI S_j^T in
@@ -2465,7 +2551,7 @@ __device__ __forceinline__ void split_items(
         if (chain) {
           chain_chunk<0>(sm, cr.c, st, wt, lane);
         } else {
-          side_chunk<0>(sm, wt, lane, scale, out_rsrc(cr), ocol, [&] {
+          side_chunk<0>(sm, wt, lane, scale, out_rsrc(i, cr), ocol, [&] {
             if (i + 1 < n) split_dma<1>(sm, chunk_ref(i + 1), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
           });
         }
@@ -2482,7 +2568,7 @@ __device__ __forceinline__ void split_items(
         if (chain) {
           chain_chunk<1>(sm, cr.c, st, wt, lane);
         } else {
-          side_chunk<1>(sm, wt, lane, scale, out_rsrc(cr), ocol, [&] {
+          side_chunk<1>(sm, wt, lane, scale, out_rsrc(i + 1, cr), ocol, [&] {
             if (i + 2 < n) split_dma<0>(sm, chunk_ref(i + 2), dl, wt, h, hq, mrun, q, k, v, ws_frag, ws_gam);
           });
         }
@@ -2512,7 +2598,9 @@ __device__ __forceinline__ void split_items(
     }
   }
 
-  if (chain && !(mrun && formed < n)) {   // a stopped M-run's map is negligible: never read
+  // a stopped M-run's map is negligible and never read; a warm-up run of a
+  // segment before the last keeps no state
+  if (chain && slot != kSlotNone && !(mrun && formed < n)) {
     if (slot < 0 || !mrun) {
       float* dst = slot < 0 ? new_state + (static_cast<size_t>(s) * kVHeads + h) * kHeadState
                             : slotb + (static_cast<size_t>(slot) * kVHeads + h) * kHeadState;
