@@ -167,6 +167,7 @@ constexpr int kSlotNone = -2;
 // chunks, so that state is formed once per block rather than once per chunk;
 // otherwise it lists one block per chunk, and the blocks run in parallel.
 constexpr int kFinThreads = 256;
+constexpr int kFinGroups = 512;   // one round at two groups per CU (the launch bounds)
 constexpr int kFinBlockChunks = 4;
 constexpr int kFinBlockSeg = 3;
 static_assert(kFinThreads / 64 == kChunk / 16, "finish tiling: one wave per 16-token tile");
@@ -569,7 +570,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     // plus a per-item overhead) bound the critical path; the scan adds half a
     // step per segment and segmenting at all 1.5 steps.  The minimum over the
     // lanes wins, ties to the longer segments.
-    float sl = 0.f, a = 0.f, runs = 0.f, nlong = 0.f;
+    float sl = 0.f, a = 0.f, runs = 0.f;
     long long slots = 0;
     int ml = 0;
     const int ci = min(lane, kSegCands - 1);
@@ -580,30 +581,21 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       a += static_cast<float>(pj[ci]);
       slots += pj[kSegCands + ci];
       runs += static_cast<float>(pj[2 * kSegCands + ci]);
-      nlong += static_cast<float>(pj[2 * kSegCands + kSegCands - 1]);   // the no-split candidate: one run each
     }
     constexpr float kItemOverhead = 1.0f;   // chunk steps per work item (metadata, state, first copies)
     const int Lc = seg_cand(ci);
     const int nseg_max = ml > 0 ? (ml - 1) / Lc + 1 : 0;
-    float est;
-    if (warm) {
-      // one run per segment (runs = sum of 2 nseg - 1 -> sum of nseg), each
-      // later segment w_est chunks longer; nothing for the finish
-      const float runs_w = 0.5f * (runs + nlong);
-      const float later = runs_w - nlong;
-      const float per_wg =
-          (16.f * (sl + static_cast<float>(w_est) * later) + kItemOverhead * 16.f * runs_w) / kConsumerGroups;
-      const float crit =
-          static_cast<float>(min(Lc, ml) + (nseg_max > 1 ? w_est : 0)) + kItemOverhead;
-      est = fmaxf(crit, per_wg);
-      // No slot is written in this scheme, but the slot bound still applies:
-      // the run table holds max_runs(N, gcap) = N + 2 gcap runs, and with at
-      // most gcap later segments the runs (one per segment) stay within it.
-    } else {
-      const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
-      const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
-      est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
-    }
+    // The same estimate serves the warm-up scheme: its later segments replace
+    // the M-runs' chunks by their warm-up chunks and item starts, and forced
+    // segment lengths on configurations 2 and 3 rank as this formula does (a
+    // model of one run per segment with the warm-up chunks preferred shorter
+    // segments than the measured best).  No slot is written in the warm-up
+    // scheme, but the slot bound below still applies: the run table holds
+    // max_runs(N, gcap) = N + 2 gcap runs, and with at most gcap later
+    // segments the runs (one per segment) stay within it.
+    const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
+    const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
+    float est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
     // Slowly decaying heads: their segment maps never become negligible, so
     // every correction block of segment j >= 2 in the finish first takes j - 1
     // scan steps.  The heads' chunk map bound is estimated from the per-head
@@ -2807,8 +2799,18 @@ __global__ __launch_bounds__(kFinThreads, 2) void finish_kernel(int* __restrict_
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int l16 = lane & 15, lg = lane >> 4;
-  // the state items first: they may step through several segment maps
-  for (int it = blockIdx.x; it < ncorr + nmulti * kVHeads; it += gridDim.x) {
+  // The state items first: they may step through several segment maps.  The
+  // grid is one round of groups (two per CU); items past it go out in
+  // alternating order, pass k taking group g's item k G + g for even k and
+  // (k + 1) G - 1 - g for odd k, so second items land on the groups whose
+  // first item was a cheap one (the last correction blocks) rather than on
+  // the state items.
+  const int G = static_cast<int>(gridDim.x);
+  const int nitem = ncorr + nmulti * kVHeads;
+  for (int pass = 0;; ++pass) {
+    const int it = (pass & 1) ? (pass + 1) * G - 1 - static_cast<int>(blockIdx.x)
+                              : pass * G + static_cast<int>(blockIdx.x);
+    if (it >= nitem) break;
     if (it < nmulti * kVHeads) {
       const int h = it & 7;
       // new_state = S_nseg
@@ -3020,7 +3022,7 @@ int prefill_launch(const void* q, const void* k, const void* v, const float* sta
       slotb, slotm, mval, fix);
   // a second segment needs more than kMinSegChunks chunks in one sequence and a slot
   if (gcap > 0 && total_tokens > static_cast<long long>(kMinSegChunks) * kChunk) {
-    const long long g_fin = std::min<long long>(R * kVHeads, 1024);
+    const long long g_fin = std::min<long long>(R * kVHeads, kFinGroups);
     finish_kernel<<<dim3(static_cast<unsigned>(g_fin)), dim3(kFinThreads), 0, st>>>(
         lists, num_seqs, gc, fix, static_cast<int>(R * kVHeads), slotb, slotm, mval, oi, ob, new_state);
   }
