@@ -168,6 +168,7 @@ constexpr int kSlotNone = -2;
 // otherwise it lists one block per chunk, and the blocks run in parallel.
 constexpr int kFinThreads = 256;
 constexpr int kFinGroups = 512;   // one round at two groups per CU (the launch bounds)
+static_assert(kFinGroups == 64 * 8, "finish item permutation: 64 items per XCD");
 constexpr int kFinBlockChunks = 4;
 constexpr int kFinBlockSeg = 3;
 static_assert(kFinThreads / 64 == kChunk / 16, "finish tiling: one wave per 16-token tile");
@@ -2805,11 +2806,16 @@ __global__ __launch_bounds__(kFinThreads, 2) void finish_kernel(int* __restrict_
   // (k + 1) G - 1 - g for odd k, so second items land on the groups whose
   // first item was a cheap one (the last correction blocks) rather than on
   // the state items.
+  // With a full grid, the group's position in the item order is permuted so
+  // that runs of 64 consecutive items (the blocks of one segment and v-head,
+  // which load the same segment state and maps) share an XCD (group id % 8)
+  // and find those in one L2.
   const int G = static_cast<int>(gridDim.x);
   const int nitem = ncorr + nmulti * kVHeads;
+  const int gid = static_cast<int>(blockIdx.x);
+  const int slot_g = G == kFinGroups ? 64 * (gid & 7) + (gid >> 3) : gid;
   for (int pass = 0;; ++pass) {
-    const int it = (pass & 1) ? (pass + 1) * G - 1 - static_cast<int>(blockIdx.x)
-                              : pass * G + static_cast<int>(blockIdx.x);
+    const int it = (pass & 1) ? (pass + 1) * G - 1 - slot_g : pass * G + slot_g;
     if (it >= nitem) break;
     if (it < nmulti * kVHeads) {
       const int h = it & 7;
