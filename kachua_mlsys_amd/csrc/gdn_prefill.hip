@@ -931,25 +931,29 @@ __device__ __forceinline__ void store_frag(const u32x4& x, uint16_t* dst) {
 // K / Q rows they hold anyway.  NB: the number of 16-token blocks that hold
 // tokens (c <= 16 NB).  Later blocks have beta = 0, so their rows of N and
 // every fragment of Tb that touches them are exactly zero: they are stored as
-// zeros without being formed.
-template <int NH, bool kToLds = false, int NB = 4>
-__device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4],
-                                              int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
-                                              const float (&alog)[kGva], const float (&dtb)[kGva],
-                                              uint16_t* __restrict__ frag0, float* __restrict__ gp0) {
+// zeros without being formed.  Two phases: prepass_gates, then prepass_terms.
+//
+// The gates of NH v-heads (the first phase of the terms; it needs only a, b
+// and the per-head constants, so it can run while the chunk's K rows are in
+// flight): Gam_t = inclusive scan of log2 g (clamped: g = e^-100 is already 0
+// to fp32 working precision, and a finite floor keeps Gam finite), beta_t;
+// gam / tail / Gam to the gate blocks, Gam and beta to ws rows 0 .. NH - 1,
+// Gam at the chunk's last token to last[].
+template <int NH, bool kToLds = false>
+__device__ __forceinline__ void prepass_gates(PrepassWaveSmem& ws, int c, const float (&a_t)[kGva],
+                                              const float (&b_t)[kGva], const float (&alog)[kGva],
+                                              const float (&dtb)[kGva], float* __restrict__ gp0,
+                                              float (&last)[NH]) {
   const int lane = threadIdx.x & 63;
-  const int l16 = lane & 15, lg = lane >> 4;
-  // per-head workspace blocks are consecutive v-heads of one record
-  constexpr size_t kFragStride = kMatElems;
-
-  // ---- gates: Gam_t = inclusive scan of log2 g (clamped: g = e^-100 is
-  // already 0 to fp32 working precision, and a finite floor keeps Gam
-  // finite), beta_t; gam / tail to the workspace ----
-  float last[NH];
 #pragma unroll
   for (int e = 0; e < NH; ++e) {
-    const float lgv = lane < c ? fmaxf(log_decay(alog[e], a_t[e], dtb[e]), -100.0f) * kLog2e : 0.0f;
-    const float bet = lane < c ? sigmoidf(b_t[e]) : 0.0f;
+    // formed on every lane (a lane past the chunk holds its last token's
+    // gates: finite), then masked: no branch for the compiler to sink the
+    // gate loads into behind the K rows' loads
+    const float lgv_all = fmaxf(log_decay(alog[e], a_t[e], dtb[e]), -100.0f) * kLog2e;
+    const float bet_all = sigmoidf(b_t[e]);
+    const float lgv = lane < c ? lgv_all : 0.0f;
+    const float bet = lane < c ? bet_all : 0.0f;
     const float lgam = wave_incl_sumf(lgv);
     last[e] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lgam), c - 1));
     float* gp = gp0 + e * kGamStride;
@@ -960,6 +964,18 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     ws.beta[e][lane] = bet;
   }
   wave_lds_sync();
+}
+
+// The rest of the terms of NH v-heads, whose gates prepass_gates left in ws
+// rows E0 .. E0 + NH - 1 (and last[]), from the chunk's raw gram.
+template <int NH, int E0 = 0, bool kToLds = false, int NB = 4>
+__device__ __forceinline__ void prepass_terms(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4], int c,
+                                              const float (&last)[NH], uint16_t* __restrict__ frag0,
+                                              float* __restrict__ gp0) {
+  const int lane = threadIdx.x & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  // per-head workspace blocks are consecutive v-heads of one record
+  constexpr size_t kFragStride = kMatElems;
   float lcol[NH][4];     // Gam at column 16 n + l16
   f32x4 lrow[NH][4];     // Gam at rows 16 m + 4 lg + rr
   f32x4 brow[NH][4];     // beta at rows 16 m + 4 lg + rr
@@ -967,9 +983,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
   for (int e = 0; e < NH; ++e)
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-      lcol[e][m] = ws.lgam[e][16 * m + l16];
-      lrow[e][m] = *reinterpret_cast<const f32x4*>(&ws.lgam[e][16 * m + 4 * lg]);
-      brow[e][m] = *reinterpret_cast<const f32x4*>(&ws.beta[e][16 * m + 4 * lg]);
+      lcol[e][m] = ws.lgam[E0 + e][16 * m + l16];
+      lrow[e][m] = *reinterpret_cast<const f32x4*>(&ws.lgam[E0 + e][16 * m + 4 * lg]);
+      brow[e][m] = *reinterpret_cast<const f32x4*>(&ws.beta[E0 + e][16 * m + 4 * lg]);
     }
 
   // ---- N = strict_lower(beta_t rho K K^T): diagonal tiles to LDS
@@ -996,7 +1012,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr)
             if (m < NB && l16 == 4 * lg + rr) kb[e] += __log2f(fmaxf(1.0f, fabsf(1.0f - brow[e][m][rr] * kk[m][m][rr])));
-          *reinterpret_cast<f32x4*>(&ws.nt[e][m][l16][4 * lg]) = nv;
+          *reinterpret_cast<f32x4*>(&ws.nt[E0 + e][m][l16][4 * lg]) = nv;
         } else {
           nlo[e][m][n] = nv;
         }
@@ -1024,7 +1040,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     f32x4 ring[kAhead][4];
     auto read_col = [&](int i, f32x4 (&c)[4]) {
 #pragma unroll
-      for (int qv = (i + 1) >> 2; qv < 4; ++qv) c[qv] = *reinterpret_cast<const f32x4*>(&ws.nt[e][lg][i][4 * qv]);
+      for (int qv = (i + 1) >> 2; qv < 4; ++qv) c[qv] = *reinterpret_cast<const f32x4*>(&ws.nt[E0 + e][lg][i][4 * qv]);
     };
 #pragma unroll
     for (int i = 0; i < kAhead; ++i) read_col(i, ring[i]);
@@ -1039,7 +1055,7 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     }
 #pragma unroll
     for (int qv = 0; qv < 4; ++qv)
-      *reinterpret_cast<f32x4*>(&ws.nt[e][lg][l16][4 * qv]) = f32x4{x[4 * qv], x[4 * qv + 1], x[4 * qv + 2], x[4 * qv + 3]};
+      *reinterpret_cast<f32x4*>(&ws.nt[E0 + e][lg][l16][4 * qv]) = f32x4{x[4 * qv], x[4 * qv + 1], x[4 * qv + 2], x[4 * qv + 3]};
   }
   wave_lds_sync();
 
@@ -1052,9 +1068,9 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
     f32x4 tc[4], w[4][4];   // tc[a] = T_aa = (W_aa)^T in C layout; w[a][b] = W_ab, a <= b
 #pragma unroll
     for (int ab = 0; ab < 4; ++ab) {
-      tc[ab] = *reinterpret_cast<const f32x4*>(&ws.nt[e][ab][l16][4 * lg]);
+      tc[ab] = *reinterpret_cast<const f32x4*>(&ws.nt[E0 + e][ab][l16][4 * lg]);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) w[ab][ab][rr] = ws.nt[e][ab][4 * lg + rr][l16];
+      for (int rr = 0; rr < 4; ++rr) w[ab][ab][rr] = ws.nt[E0 + e][ab][4 * lg + rr][l16];
     }
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     // operands split once: tx[a] from T_aa, nx[m][a] from N_ma = U_am^T,
@@ -1129,6 +1145,17 @@ __device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (
   }
 }
 
+// Gates and terms of NH v-heads in one go (the direct path).
+template <int NH, bool kToLds = false, int NB = 4>
+__device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4],
+                                              int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
+                                              const float (&alog)[kGva], const float (&dtb)[kGva],
+                                              uint16_t* __restrict__ frag0, float* __restrict__ gp0) {
+  float last[NH];
+  prepass_gates<NH, kToLds>(ws, c, a_t, b_t, alog, dtb, gp0, last);
+  prepass_terms<NH, 0, kToLds, NB>(ws, kk, c, last, frag0, gp0);
+}
+
 // Raw gram of one chunk (rows t0 .. t0 + c - 1 of q/k head hq), one wave:
 // kk = K K^T (lower tiles, kk[m][n] = [t = 16 m + 4 lg + rr][i = 16 n + l16]).
 // Fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
@@ -1170,6 +1197,37 @@ __device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ k, long
   }
 }
 
+// The raw gram in two steps for the prepass kernel: every fragment of the
+// chunk's K rows requested at once (one memory round trip; the gates are
+// formed while they are in flight), then the products.  Same rows, clamping
+// and products as chunk_grams.
+__device__ __forceinline__ void chunk_gram_loads(const uint16_t* __restrict__ k, long long t0, int c, int hq,
+                                                 int lane, bf16x8 (&kf)[4][4]) {
+  const int l16 = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, c - 1));
+    const uint16_t* krow = k + (row * kQKHeads + hq) * kDim + 8 * lg;
+#pragma unroll
+    for (int dd = 0; dd < 4; ++dd) kf[dd][m] = *reinterpret_cast<const bf16x8*>(krow + 32 * dd);
+  }
+}
+__device__ __forceinline__ void chunk_gram_products(const bf16x8 (&kf)[4][4], f32x4 (&kk)[4][4]) {
+  // the products wait for K: nothing formed before this point (the gates)
+  // may be scheduled behind them
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int n = 0; n <= m; ++n) kk[m][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int dd = 0; dd < 4; ++dd)
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int n = 0; n <= m; ++n) kk[m][n] = mfma16(kf[dd][m], kf[dd][n], kk[m][n]);
+}
+
 // kGroups: work-groups per CU the register budget is sized for (2, or 3 for
 // one-v-head items in batches of 2048-3072 of them).
 template <bool kPair, int kGroups>
@@ -1189,6 +1247,8 @@ __global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
     return;
   }
   const int lane = threadIdx.x & 63;
+  // the per-head constants, requested first: lane l holds v-head l & 7's
+  const float alog_l = A_log[lane & 7], dtb_l = dt_bias[lane & 7];
   const int wv = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
   PrepassWaveSmem& ws = sm.u.w[wv];
   const int gw = (static_cast<int>(blockIdx.x) - fused_plan) * kPrepassWaves + wv;
@@ -1283,8 +1343,9 @@ __global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
     const int c = static_cast<int>(min(static_cast<long long>(kChunk), s1 - t0));
     const int cm1 = c - 1;
 
-    // ---- loads: gates (lane = token, clamped into the chunk), then the raw
-    // grams, shared by the v-heads of the pair ----
+    // ---- loads: gates (lane = token, clamped into the chunk), then every
+    // fragment of the K rows (shared by the v-heads of the pair); the gates
+    // are formed while K is in flight ----
     const size_t gi = static_cast<size_t>(t0 + min(lane, cm1)) * kVHeads + kGva * hq + e0;
     float a_t[kGva], b_t[kGva];
 #pragma unroll
@@ -1292,25 +1353,34 @@ __global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
       a_t[e] = e < ne ? bf2f(a[gi + e]) : 0.0f;
       b_t[e] = e < ne ? bf2f(b[gi + e]) : 0.0f;
     }
-    f32x4 kk[4][4];
-    chunk_grams(k, t0, c, hq, lane, kk);
+    bf16x8 kf[4][4];
+    chunk_gram_loads(k, t0, c, hq, lane, kf);
 
     const int h0 = kGva * hq + e0;
     float alog[kGva], dtb[kGva];
 #pragma unroll
     for (int e = 0; e < kGva; ++e) {
-      alog[e] = A_log[min(h0 + e, kVHeads - 1)];
-      dtb[e] = dt_bias[min(h0 + e, kVHeads - 1)];
+      const int hh = min(h0 + e, kVHeads - 1);
+      alog[e] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alog_l), hh));
+      dtb[e] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dtb_l), hh));
     }
     uint16_t* frag0 = ws_frag + (static_cast<size_t>(r) * kVHeads + h0) * kMatElems;
     float* gp0 = ws_gam + (static_cast<size_t>(r) * kVHeads + h0) * kGamStride;
-    // the v-heads of a pair one after the other (interleaving their phases
-    // gains nothing: the phases are VALU-bound, not latency-bound)
-    for (int e = 0; e < ne; ++e) {
-      const float a1[kGva] = {e == 0 ? a_t[0] : a_t[1], 0.0f}, b1[kGva] = {e == 0 ? b_t[0] : b_t[1], 0.0f};
-      const float al1[kGva] = {e == 0 ? alog[0] : alog[1], 0.0f}, dt1[kGva] = {e == 0 ? dtb[0] : dtb[1], 0.0f};
-      prepass_heads<1>(ws, kk, c, a1, b1, al1, dt1, frag0 + e * static_cast<size_t>(kMatElems),
-                       gp0 + e * kGamStride);
+    f32x4 kk[4][4];
+    if constexpr (pair_items) {
+      float last[kGva];
+      prepass_gates<kGva>(ws, c, a_t, b_t, alog, dtb, gp0, last);
+      chunk_gram_products(kf, kk);
+      // the v-heads of the pair one after the other (interleaving their
+      // phases gains nothing: the phases are VALU-bound, not latency-bound)
+      const float l0[1] = {last[0]}, l1[1] = {last[1]};
+      prepass_terms<1, 0>(ws, kk, c, l0, frag0, gp0);
+      prepass_terms<1, 1>(ws, kk, c, l1, frag0 + kMatElems, gp0 + kGamStride);
+    } else {
+      float last[1];
+      prepass_gates<1>(ws, c, a_t, b_t, alog, dtb, gp0, last);
+      chunk_gram_products(kf, kk);
+      prepass_terms<1, 0>(ws, kk, c, last, frag0, gp0);
     }
   }
 }
