@@ -1145,85 +1145,40 @@ __device__ __forceinline__ void prepass_terms(PrepassWaveSmem& ws, const f32x4 (
   }
 }
 
-// Gates and terms of NH v-heads in one go (the direct path).
-template <int NH, bool kToLds = false, int NB = 4>
-__device__ __forceinline__ void prepass_heads(PrepassWaveSmem& ws, const f32x4 (&kk)[4][4],
-                                              int c, const float (&a_t)[kGva], const float (&b_t)[kGva],
-                                              const float (&alog)[kGva], const float (&dtb)[kGva],
-                                              uint16_t* __restrict__ frag0, float* __restrict__ gp0) {
-  float last[NH];
-  prepass_gates<NH, kToLds>(ws, c, a_t, b_t, alog, dtb, gp0, last);
-  prepass_terms<NH, 0, kToLds, NB>(ws, kk, c, last, frag0, gp0);
-}
-
 // Raw gram of one chunk (rows t0 .. t0 + c - 1 of q/k head hq), one wave:
 // kk = K K^T (lower tiles, kk[m][n] = [t = 16 m + 4 lg + rr][i = 16 n + l16]).
 // Fragment (m, d) of a 64x128 row block: lane (lg, l16) holds row 16 m + l16,
 // columns 32 d + 8 lg .. + 7.  Rows past the chunk end repeat row c - 1: they
 // meet beta = 0 (rows of N) and i <= t masks.  Only the tiles of the first NB
 // 16-row blocks are formed.
+// The gram comes in two steps: every fragment of the chunk's K rows requested
+// at once (one memory round trip; the gates are formed while they are in
+// flight), then the products.
 template <int NB = 4>
-__device__ __forceinline__ void chunk_grams(const uint16_t* __restrict__ k, long long t0, int c, int hq, int lane,
-                                            f32x4 (&kk)[4][4]) {
-  const int l16 = lane & 15, lg = lane >> 4;
-  const int cm1 = c - 1;
-  const uint16_t* krow[NB];
-#pragma unroll
-  for (int m = 0; m < NB; ++m) {
-    const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, cm1));
-    krow[m] = k + (row * kQKHeads + hq) * kDim + 8 * lg;
-  }
-#pragma unroll
-  for (int m = 0; m < NB; ++m)
-#pragma unroll
-    for (int n = 0; n <= m; ++n) kk[m][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // the rows' fragments by depth chunk, two chunks in flight: chunk dd + 2 is
-  // loaded into chunk dd's registers once its products are issued (half the
-  // operand registers of loading all four at once)
-  bf16x8 kf[2][NB];
-  auto load_dd = [&](int dd) {
-#pragma unroll
-    for (int m = 0; m < NB; ++m) kf[dd & 1][m] = *reinterpret_cast<const bf16x8*>(krow[m] + 32 * dd);
-  };
-  load_dd(0);
-  load_dd(1);
-#pragma unroll
-  for (int dd = 0; dd < 4; ++dd) {
-#pragma unroll
-    for (int m = 0; m < NB; ++m)
-#pragma unroll
-      for (int n = 0; n <= m; ++n) kk[m][n] = mfma16(kf[dd & 1][m], kf[dd & 1][n], kk[m][n]);
-    if (dd + 2 < 4) load_dd(dd + 2);
-  }
-}
-
-// The raw gram in two steps for the prepass kernel: every fragment of the
-// chunk's K rows requested at once (one memory round trip; the gates are
-// formed while they are in flight), then the products.  Same rows, clamping
-// and products as chunk_grams.
 __device__ __forceinline__ void chunk_gram_loads(const uint16_t* __restrict__ k, long long t0, int c, int hq,
                                                  int lane, bf16x8 (&kf)[4][4]) {
   const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < NB; ++m) {
     const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, c - 1));
     const uint16_t* krow = k + (row * kQKHeads + hq) * kDim + 8 * lg;
 #pragma unroll
     for (int dd = 0; dd < 4; ++dd) kf[dd][m] = *reinterpret_cast<const bf16x8*>(krow + 32 * dd);
   }
 }
+template <int NB = 4>
 __device__ __forceinline__ void chunk_gram_products(const bf16x8 (&kf)[4][4], f32x4 (&kk)[4][4]) {
   // the products wait for K: nothing formed before this point (the gates)
   // may be scheduled behind them
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int m = 0; m < 4; ++m)
+  for (int m = 0; m < NB; ++m)
 #pragma unroll
     for (int n = 0; n <= m; ++n) kk[m][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int dd = 0; dd < 4; ++dd)
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
+    for (int m = 0; m < NB; ++m)
 #pragma unroll
       for (int n = 0; n <= m; ++n) kk[m][n] = mfma16(kf[dd][m], kf[dd][n], kk[m][n]);
 }
@@ -1959,9 +1914,13 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
     // only the 16-token blocks that hold tokens are formed (c <= 16 nb)
     auto blocks = [&](auto NBC) {
       constexpr int NB = decltype(NBC)::value;
+      bf16x8 kf[4][4];
+      chunk_gram_loads<NB>(k, c0, c, hq, lane, kf);
+      float last[1];
+      prepass_gates<1, true>(sm.w[J], c, a1, b1, al1, dt1, &sm.c.gt[J][0], last);
       f32x4 kk[4][4];
-      chunk_grams<NB>(k, c0, c, hq, lane, kk);
-      prepass_heads<1, true, NB>(sm.w[J], kk, c, a1, b1, al1, dt1, &sm.c.frag[J][0][0], &sm.c.gt[J][0]);
+      chunk_gram_products<NB>(kf, kk);
+      prepass_terms<1, 0, true, NB>(sm.w[J], kk, c, last, &sm.c.frag[J][0][0], &sm.c.gt[J][0]);
     };
     switch ((c + 15) >> 4) {
       case 1: blocks(std::integral_constant<int, 1>{}); break;
