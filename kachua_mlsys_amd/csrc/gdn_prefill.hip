@@ -1540,6 +1540,18 @@ __device__ __forceinline__ void fh_aqk(ConsumerSmem& sm, int lane, int c) {
   }
 }
 
+// Calls f with the number of 16-token tiles that hold a chunk's c >= 1 tokens,
+// as a compile-time constant (uniform branch).
+template <class F>
+__device__ __forceinline__ void chunk_by_tiles(int c, F&& f) {
+  switch ((c + 15) >> 4) {
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 3: f(std::integral_constant<int, 3>{}); break;
+    default: f(std::integral_constant<int, 4>{}); break;
+  }
+}
+
 // One chunk of the recurrence for the 16-wide V tile of this wave.
 //   st : S^T tile in C layout with a k order chosen for the K row reads:
 //        st[kt][rr] = S[v0 + l16][kappa(kt, lg, rr)],
@@ -1549,10 +1561,17 @@ __device__ __forceinline__ void fh_aqk(ConsumerSmem& sm, int lane, int c) {
 //   orc : buffer resource over the chunk's output rows [c0, c0 + c) of this head
 //         (num_records = c rows, so stores of rows t >= c are dropped by the
 //         range check: no branch); ocol = byte offset of value column v0 + 4 lg.
-template <int P>
+//   NB  : 16-token tiles that hold tokens (c <= 16 NB).  Rows t >= c have
+//         beta = 0 and gam = tail = 0, so the later tiles contribute nothing
+//         (zero columns of Tb, zero rows of Delta); their products are not
+//         formed (their R rows count as zero, also for R's range scale), and
+//         the state update skips the second 32-token depth half when NB <= 2.
+template <int P, int NB>
 __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&st)[8], int w,
                                                int lane, float scale, __amdgpu_buffer_rsrc_t orc,
                                                uint32_t ocol) {
+  static_assert(NB >= 1 && NB <= 4, "token tiles");
+  constexpr int ND = (NB + 1) / 2;   // 32-token depth halves that hold tokens
   const int l16 = lane & 15, lg = lane >> 4;
   // ---- this wave's Aqk tiles, first (fewest registers live); every wave
   // reads them after the barrier before O^T ----
@@ -1586,6 +1605,7 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
   for (int m = 0; m < 4; ++m) {
     X[m] = f32x4{0.f, 0.f, 0.f, 0.f};
     YT[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (m >= NB) continue;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       const int at = 8 * ((4 * d + lg) ^ rsw);
@@ -1603,6 +1623,8 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
   f32x4 Rt[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
+    Rt[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (m >= NB) continue;
     const u32x2 vw = lds_tr16(&sm.vs[P][16 * m + vrow][vat]);
     const float vv[4] = {bf_lo(vw.x), bf_hi(vw.x), bf_lo(vw.y), bf_hi(vw.y)};
 #pragma unroll
@@ -1615,7 +1637,7 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
   }
   f16x8 rf[2];
 #pragma unroll
-  for (int d = 0; d < 2; ++d) {
+  for (int d = 0; d < ND; ++d) {
     float x[8];
     gather_slots(Rt, d, x);
     rf[d] = half_frag(x);
@@ -1624,8 +1646,9 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     D[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (m >= NB) continue;
 #pragma unroll
-    for (int d = 0; d < 2; ++d)
+    for (int d = 0; d < ND; ++d)
       if (!frag_zero(m, d))
         D[m] = mfma16h(*reinterpret_cast<const f16x8*>(&sm.frag[P][0][(frag_slot(m, d) * 64 + lane) * 8]), rf[d], D[m]);
   }
@@ -1642,9 +1665,9 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
     f32x4 Dt[4];
 #pragma unroll
     for (int m = 0; m < 4; ++m)
-      Dt[m] = D[m] * *reinterpret_cast<const f32x4*>(&sm.gt[P][kChunk + 16 * m + 4 * lg]);
+      Dt[m] = m < NB ? D[m] * *reinterpret_cast<const f32x4*>(&sm.gt[P][kChunk + 16 * m + 4 * lg]) : D[m];
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
+    for (int d = 0; d < ND; ++d) {
       float x[8];
       gather_slots(D, d, x);
       dob[d] = round_frag(x);
@@ -1657,10 +1680,10 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
   //      16m + l16, value columns 4lg .. 4lg+3 -> one 8-byte store ----
   lds_barrier();   // every wave's Aqk tiles are in LDS
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
+  for (int m = 0; m < NB; ++m) {
     f32x4 OT = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int d = 0; d < 2; ++d)
+    for (int d = 0; d < ND; ++d)
       if (!frag_zero(m, d))
         OT = mfma16(dob[d], *reinterpret_cast<const bf16x8*>(&sm.frag[P][1][(frag_slot(m, d) * 64 + lane) * 8]), OT);
     const int t = 16 * m + l16;
@@ -1681,7 +1704,7 @@ __device__ __forceinline__ void consumer_chunk(ConsumerSmem& sm, int c, f32x4 (&
     f32x4 acc = st[kt] * gam_c;
     const int at = 8 * ((4 * (kt >> 1) + (sl & 3)) ^ tsw) + 4 * (kt & 1);
 #pragma unroll
-    for (int d = 0; d < 2; ++d) {
+    for (int d = 0; d < ND; ++d) {
       const int ta = perm_depth(d, lg, sl >> 2);
       const u32x2 a0 = lds_tr16(&sm.ks[P][ta][at]);
       const u32x2 a1 = lds_tr16(&sm.ks[P][ta + 16][at]);
@@ -1805,7 +1828,9 @@ __device__ __forceinline__ void full_head_items(
     if (cur.rec >= 0 && cur.c > 0) {
       const __amdgpu_buffer_rsrc_t orc = __builtin_amdgcn_make_buffer_rsrc(
           out + (static_cast<size_t>(cur.c0) * kVHeads + cur.h) * kDim, 0, cur.c * (kVHeads * kDim * 2), 0x00020000);
-      consumer_chunk<P>(sm, cur.c, st, w, lane, scale, orc, ocol);
+      // all four tiles: batches of many short sequences are bound by their
+      // state traffic, and one body keeps the loop's code small
+      consumer_chunk<P, 4>(sm, cur.c, st, w, lane, scale, orc, ocol);
     }
     // an empty sequence leaves new_state zero (st is zero); a chunk without a
     // record (malformed cu_seqlens) passes the state through.  State bytes are
@@ -1939,8 +1964,15 @@ __global__ __launch_bounds__(kConsumerThreads) void direct_kernel(
                                              chunk_len(j) * (kVHeads * kDim * 2), 0x00020000);
   };
   // each wave carries its own state tile: no barrier between the chunks
-  consumer_chunk<0>(sm.c, chunk_len(0), st, w, lane, scale, out_rsrc(0), ocol);
-  if (nch > 1) consumer_chunk<1>(sm.c, chunk_len(1), st, w, lane, scale, out_rsrc(1), ocol);
+  if (nch > 1) {
+    consumer_chunk<0, 4>(sm.c, chunk_len(0), st, w, lane, scale, out_rsrc(0), ocol);
+    consumer_chunk<1, 4>(sm.c, chunk_len(1), st, w, lane, scale, out_rsrc(1), ocol);
+  } else {
+    // a lone chunk (short prompts): only its tiles that hold tokens
+    chunk_by_tiles(chunk_len(0), [&](auto NBC) {
+      consumer_chunk<0, decltype(NBC)::value>(sm.c, chunk_len(0), st, w, lane, scale, out_rsrc(0), ocol);
+    });
+  }
 #pragma unroll
   for (int kt = 0; kt < 8; ++kt) __builtin_nontemporal_store(st[kt], reinterpret_cast<f32x4*>(dst + kappa0(kt)));
 }

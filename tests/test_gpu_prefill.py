@@ -73,11 +73,14 @@ def test_prefill_partial_chunk_blocks(gpu):
 @pytest.mark.parametrize("lengths,zero_state,cu64", [
     ([16], False, False), ([64], True, False), ([10, 0, 20, 34], False, True), ([1] * 64, False, False),
     ([0, 0, 0, 5, 0], True, True), ([0, 0], False, False), ([128], False, False), ([100, 28], False, True),
-    ([65, 0, 63], True, False), ([17, 111], False, False)])
+    ([65, 0, 63], True, False), ([17, 111], False, False),
+    ([15, 16, 17, 31, 32], False, False), ([33, 47, 48], True, False), ([49, 63, 1], False, True)])
 def test_prefill_direct(gpu, lengths, zero_state, cu64):
     # at most 128 tokens and 64 sequences in the call: the single-launch
     # direct path (each chunk's terms formed in LDS by one wave, then the
-    # chunks), no workspace use
+    # chunks), no workspace use.  A sequence of one chunk runs only the
+    # 16-token tiles that hold tokens: lone chunks on both sides of every
+    # tile boundary.
     p = prefill_inputs_from_lengths(lengths, seed=len(lengths) * 7 + sum(lengths), zero_state=zero_state,
                                     cu_dtype=torch.int64 if cu64 else torch.int32)
     _check(p, gpu, f"prefill direct {lengths[:8]} zero_state={zero_state} int64={cu64}")
