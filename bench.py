@@ -315,9 +315,11 @@ def chain_step_us(args, torch, dev) -> dict:
 
 # Prefill workloads beside the three configurations: configuration 3 with
 # near-1 decay (every chunk takes the state's bf16 lo pass, and the segment
-# maps stay large), and one-sequence prompts of 16, 64 and 128 tokens, where a
-# call is launch-bound (the direct path).
-EXTRA_PREFILL = ("c3_slow_decay", "t16", "t64", "t128")
+# maps stay large), one-sequence prompts of 16, 64 and 128 tokens, where a
+# call is launch-bound (the direct path), and long prompts (2 x 8192 and
+# 4 x 16384 tokens), where the segment length sets the critical path.
+EXTRA_PREFILL = ("c3_slow_decay", "t16", "t64", "t128", "long2x8192", "long4x16384")
+WARM_EXTRA = ("t16", "t64", "t128")   # timed on one buffer set (a few hundred KB)
 
 
 def extra_prefill_inputs(name):
@@ -335,6 +337,10 @@ def extra_prefill_inputs(name):
         return prefill_inputs_from_lengths([64], seed=64)
     if name == "t128":
         return prefill_inputs_from_lengths([128], seed=128)
+    if name == "long2x8192":
+        return prefill_inputs_from_lengths([8192, 8192], seed=8192)
+    if name == "long4x16384":
+        return prefill_inputs_from_lengths([16384] * 4, seed=16384)
     raise ValueError(f"unknown extra prefill workload {name!r} (known: {', '.join(EXTRA_PREFILL)})")
 
 
@@ -527,9 +533,10 @@ def main():
             extra = "" if args.profile else ",".join(EXTRA_PREFILL)
         for name in (x.strip() for x in extra.split(",") if x.strip()):
             p_cpu = extra_prefill_inputs(name)
-            e = time_prefill(p_cpu, args, torch, dev, warm=name != "c3_slow_decay")
+            e = time_prefill(p_cpu, args, torch, dev, warm=name in WARM_EXTRA)
             pre[name] = {k: e[k] for k in ("tokens", "seqs", "max_len", "us_per_call",
-                                           "us_per_call_eager_python_loop", "tokens_per_s", "cache")}
+                                           "us_per_call_eager_python_loop", "tokens_per_s", "cache",
+                                           "segment_chunks")}
             pre[name]["roofline_frac"] = e["roofline"]["frac"]
         if step is not None:
             pre["chain_step"] = step

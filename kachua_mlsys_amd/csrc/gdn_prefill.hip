@@ -450,7 +450,7 @@ __device__ __forceinline__ SeqPlan seq_plan(int nch, int L, bool warm) {
 }
 
 // Scratch ints used by plan_batch.
-constexpr int kPsVals = 3 * kSegCands + 2;
+constexpr int kPsVals = 3 * kSegCands + 3;
 constexpr int kPsCand = 0;                                   // [waves][kPsVals]
 constexpr int kPsScan = kPsCand + (kPlanThreads / 64) * kPsVals;   // [waves][5]
 constexpr int kPsHist = kPsScan + (kPlanThreads / 64) * 5;
@@ -465,12 +465,15 @@ constexpr int kPlanScratch = kPsMisc + 4;
 // sequences), the scan (multi-segment sequences) and the correction (segments
 // >= 1).
 //
-// Segment length: for each candidate L the split consumer's critical path is
-// about max(L + o, (16 W(L) + 16 o runs(L)) / groups) chunk steps, W(L) = sum
-// over long sequences of (2 nch - min(nch, L)) chunk runs per (value half,
-// v-head), o the per-item overhead; the scan adds about half a chunk step per
-// segment and segmenting at all about 1.5 steps.  Candidates whose segments
-// would not fit the workspace slots are skipped.
+// Segment length: for each candidate L an estimate of the split consumer's
+// critical path in chunk steps, the smallest winning (ties to the longer L).
+// With M-runs: max(L + o, (16 W(L) + 16 o runs(L)) / groups), W(L) = sum over
+// long sequences of (2 nch - min(nch, L)) chunk runs per (value half, v-head),
+// o the per-item overhead, plus about half a step per segment for the scan and
+// 1.5 for segmenting at all (and a scan term for slowly decaying heads).  With
+// warm-up runs: the runs' list schedule on groups / 16 machines (longest run
+// or balanced load plus a last-round tail; see the evaluation below).
+// Candidates whose segments would not fit the workspace slots are skipped.
 // Returns the thread's first record index.  t0_first / t1_first: bounds of the
 // thread's first sequence when the caller already read them (t1_first < 0:
 // not known).
@@ -513,12 +516,13 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
   int A[kSegCands], B[kSegCands], C[kSegCands];
 #pragma unroll
   for (int i = 0; i < kSegCands; ++i) A[i] = B[i] = C[i] = 0;
-  int suml = 0, maxl = 0;
+  int suml = 0, maxl = 0, nlong = 0;
   for (int s = s_begin; s < s_end; ++s) {
     const int nch = chunks(s);
     if (nch < kLongChunks) continue;
     suml += nch;
     maxl = max(maxl, nch);
+    ++nlong;
 #pragma unroll
     for (int i = 0; i < kSegCands; ++i) {
       const int Lc = seg_cand(i);
@@ -538,6 +542,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     }
     suml = wave_sum(suml);
     maxl = wave_max0(maxl);
+    nlong = wave_sum(nlong);
   }
   if (lane == 0) {
     int* pw = ps + kPsCand + wv * kPsVals;
@@ -549,6 +554,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     }
     pw[3 * kSegCands] = suml;
     pw[3 * kSegCands + 1] = maxl;
+    pw[3 * kSegCands + 2] = nlong;
   }
   for (int i = tid; i < 2 * kBuckets; i += NT) ps[kPsHist + i] = 0;
   __syncthreads();
@@ -571,7 +577,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     // plus a per-item overhead) bound the critical path; the scan adds half a
     // step per segment and segmenting at all 1.5 steps.  The minimum over the
     // lanes wins, ties to the longer segments.
-    float sl = 0.f, a = 0.f, runs = 0.f;
+    float sl = 0.f, a = 0.f, runs = 0.f, nl = 0.f;
     long long slots = 0;
     int ml = 0;
     const int ci = min(lane, kSegCands - 1);
@@ -579,6 +585,7 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
       const int* pj = ps + kPsCand + j * kPsVals;
       sl += static_cast<float>(pj[3 * kSegCands]);
       ml = max(ml, pj[3 * kSegCands + 1]);
+      nl += static_cast<float>(pj[3 * kSegCands + 2]);
       a += static_cast<float>(pj[ci]);
       slots += pj[kSegCands + ci];
       runs += static_cast<float>(pj[2 * kSegCands + ci]);
@@ -586,17 +593,33 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     constexpr float kItemOverhead = 1.0f;   // chunk steps per work item (metadata, state, first copies)
     const int Lc = seg_cand(ci);
     const int nseg_max = ml > 0 ? (ml - 1) / Lc + 1 : 0;
-    // The same estimate serves the warm-up scheme: its later segments replace
-    // the M-runs' chunks by their warm-up chunks and item starts, and forced
-    // segment lengths on configurations 2 and 3 rank as this formula does (a
-    // model of one run per segment with the warm-up chunks preferred shorter
-    // segments than the measured best).  No slot is written in the warm-up
-    // scheme, but the slot bound below still applies: the run table holds
-    // max_runs(N, gcap) = N + 2 gcap runs, and with at most gcap later
-    // segments the runs (one per segment) stay within it.
-    const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
-    const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
-    float est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    float est;
+    if (warm) {
+      // Warm-up scheme: one run per segment (T of them), each later segment
+      // W chunks longer; the work-groups take a run's 16 items together, so
+      // the packing is that of T runs on kConsumerGroups / 16 machines:
+      // the longest run, or the balanced load plus a quarter of an average
+      // run for the last round when there is more than one.  Item overhead
+      // (descriptor, warm-up bounds, first copies, final stores) about 1.5
+      // chunk steps.  Fitted with a list-scheduling model of the consumer
+      // against its measured step and item costs (c3: L = 18, 2 x 8192
+      // tokens: 16, 4 x 16384: 64, all measured faster than the earlier
+      // estimate's 20, 28 and 96).
+      constexpr float kWarmItem = 1.5f, kTailShare = 0.25f, kSegmented = 0.75f;
+      constexpr float kMachines = static_cast<float>(kConsumerGroups / 16);
+      const float T = 0.5f * (runs + nl);                      // runs = sum of 2 nseg - 1
+      const float work = sl + static_cast<float>(w_est) * (T - nl);
+      const float longest = ml > Lc ? static_cast<float>(Lc + w_est) : static_cast<float>(ml);
+      const float balanced = (work + kWarmItem * T) / kMachines;
+      const float tail = T > kMachines ? kTailShare * (work / fmaxf(T, 1.f) + kWarmItem) : 0.f;
+      est = fmaxf(longest + kWarmItem, balanced + tail) + (nseg_max > 1 ? kSegmented : 0.f);
+    } else {
+      // M-run scheme: W(L) counts the M-runs of later segments.  The scan
+      // adds about half a step per segment and segmenting at all 1.5 steps.
+      const float per_wg = (16.f * (2.f * sl - a) + kItemOverhead * 16.f * runs) / kConsumerGroups;
+      const float crit = static_cast<float>(min(Lc, ml)) + kItemOverhead;
+      est = fmaxf(crit, per_wg) + (nseg_max > 1 ? 0.5f * static_cast<float>(nseg_max - 1) + 1.5f : 0.f);
+    }
     // Slowly decaying heads: their segment maps never become negligible, so
     // every correction block of segment j >= 2 in the finish first takes j - 1
     // scan steps.  The heads' chunk map bound is estimated from the per-head
@@ -612,7 +635,11 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
                        static_cast<float>(last) * static_cast<float>(nseg_max - 2);
       est += slow_frac * kScanStepCost * pj;
     }
-    // key: estimate in 1/16 steps, then the longer candidate; invalid lanes hold the maximum
+    // key: estimate in 1/16 steps, then the longer candidate; invalid lanes hold
+    // the maximum.  No slot is written in the warm-up scheme, but the slot
+    // bound still applies: the run table holds max_runs(N, gcap) = N + 2 gcap
+    // runs, and with at most gcap later segments the runs (one per segment)
+    // stay within it.
     const int q = static_cast<int>(fminf(est * 16.f, 1.0e7f));
     const int key = (lane < kSegCands && slots <= gcap) ? q * 64 + (63 - lane) : 0x7fffffff;
     // minimum over the lanes: the maximum of the complements
