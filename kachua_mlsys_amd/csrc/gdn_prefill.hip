@@ -109,7 +109,7 @@ constexpr int kMatElems = kMatFrags * kFragTile;   // one packed 64x64 matrix
 // V = 0 (outputs OI, final state M_j).  The recurrence is linear in (S, V), so
 //   S_{j+1} = S_j M_j + B_j,          O_j = O0_j + OI_j S_j^T,
 // which a short scan over segments and a parallel correction pass resolve.
-constexpr int kMinSegChunks = 4;   // shortest segment the planner may choose
+constexpr int kMinSegChunks = 4;   // shortest M-run segment (the warm-up scheme may take 2 or 3)
 constexpr int kMSlotElems = 8 * 4 * 2 * 64 * 8;   // M_j^T as bf16 hi / lo MFMA fragments, per head
 
 // Upper bound on the segments of all multi-segment sequences: a sequence of
@@ -407,11 +407,15 @@ __device__ __forceinline__ void block_scan_v(int (&x)[K], int* wave_tot, int (&t
   __syncthreads();
 }
 
-// Candidate segment lengths (chunks): 4, 6, ..., 32, then 40, 48, 64, 80,
-// 96, 128, ... (5, 6, 8 x 2^k) up to 1024, and "no split".
-constexpr int kSegCands = 31;
+// Candidate segment lengths (chunks): 2, 3 (warm-up batches only), 4, 6, ...,
+// 32, then 40, 48, 64, 80, 96, 128, ... (5, 6, 8 x 2^k) up to 1024, and "no
+// split", in increasing order.
+constexpr int kSegCands = 33;
+constexpr int kShortCands = 2;   // the candidates below kMinSegChunks
 __device__ __forceinline__ int seg_cand(int i) {
   if (i >= kSegCands - 1) return 1 << 30;
+  if (i < kShortCands) return 2 + i;
+  i -= kShortCands;
   if (i < 15) return 4 + 2 * i;
   const int j = i - 15, m = j % 3;
   return (m == 0 ? 5 : (m == 1 ? 6 : 8)) << (3 + j / 3);
@@ -641,7 +645,10 @@ __device__ int plan_batch(const void* __restrict__ cu, int is64, int num_seqs, l
     // runs, and with at most gcap later segments the runs (one per segment)
     // stay within it.
     const int q = static_cast<int>(fminf(est * 16.f, 1.0e7f));
-    const int key = (lane < kSegCands && slots <= gcap) ? q * 64 + (63 - lane) : 0x7fffffff;
+    // segments below kMinSegChunks only without M-runs (the workspace's slots
+    // are sized for M-run segments of at least kMinSegChunks)
+    const bool allowed = lane < kSegCands && slots <= gcap && (warm || Lc >= kMinSegChunks);
+    const int key = allowed ? q * 64 + (63 - lane) : 0x7fffffff;
     // minimum over the lanes: the maximum of the complements
     const int best = 0x7fffffff - wave_max0(0x7fffffff - key);
     if (lane == 0) {

@@ -47,8 +47,10 @@ def test_prefill_reference_shapes(gpu, n):
     _check(prefill_inputs_from_lengths(lengths, gen=gen), gpu, f"reference shape N={n}")
 
 
+# [200] and [190, 300, 129]: short prompts that the planner cuts into segments
+# of two chunks (warm-up runs read the bounds of at most two earlier chunks)
 @pytest.mark.parametrize("lengths", [[1], [63], [64], [65], [0, 1, 63, 64, 65, 0, 130],
-                                     [200, 0, 0, 3], [0]])
+                                     [200, 0, 0, 3], [0], [200], [190, 300, 129]])
 def test_prefill_ragged(gpu, lengths):
     _check(prefill_inputs_from_lengths(lengths, seed=len(lengths) * 31 + sum(lengths)), gpu,
            f"prefill ragged {lengths}")
