@@ -1188,17 +1188,40 @@ __device__ __forceinline__ void prepass_terms(PrepassWaveSmem& ws, const f32x4 (
 // The gram comes in two steps: every fragment of the chunk's K rows requested
 // at once (one memory round trip; the gates are formed while they are in
 // flight), then the products.
-template <int NB = 4>
+// ND: the depth chunks loaded into kf[0 .. ND - 1], from depth chunk d0 on
+// (all four by default).  The gram sums over depth chunks, so the slot a
+// depth chunk occupies does not matter as long as every slot holds one.
+template <int NB = 4, int ND = 4>
 __device__ __forceinline__ void chunk_gram_loads(const uint16_t* __restrict__ k, long long t0, int c, int hq,
-                                                 int lane, bf16x8 (&kf)[4][4]) {
+                                                 int lane, bf16x8 (&kf)[4][4], int d0 = 0) {
   const int l16 = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int m = 0; m < NB; ++m) {
     const size_t row = static_cast<size_t>(t0 + min(16 * m + l16, c - 1));
-    const uint16_t* krow = k + (row * kQKHeads + hq) * kDim + 8 * lg;
+    const uint16_t* krow = k + (row * kQKHeads + hq) * kDim + 8 * lg + 32 * d0;
 #pragma unroll
-    for (int dd = 0; dd < 4; ++dd) kf[dd][m] = *reinterpret_cast<const bf16x8*>(krow + 32 * dd);
+    for (int dd = 0; dd < ND; ++dd) kf[dd][m] = *reinterpret_cast<const bf16x8*>(krow + 32 * dd);
   }
+}
+
+// The two waves of a GVA pair (items 2j, 2j + 1 of one record on adjacent
+// waves of a work-group) each load half of the chunk's K fragments (depth
+// chunks 2 (item & 1) and 2 (item & 1) + 1, into slots 0 and 1) and trade them
+// through LDS into slots 2 and 3.  The exchange area is the wave's N-block
+// area (8 KB, unused until the terms), fragment f = 4 slot + m at
+// 16 (64 f + lane).  Two work-group barriers: the halves written, then read
+// (before any terms overwrite them).  Every wave of the group takes part: a
+// pair's items exist together (items come 8 per record), and waves without an
+// item have ended.
+static_assert(sizeof(PrepassWaveSmem::nt) >= 8 * 64 * sizeof(u32x4), "the exchange area holds eight fragments");
+__device__ __forceinline__ void trade_gram_halves(u32x4* mine, const u32x4* partner, int lane,
+                                                  bf16x8 (&kf)[4][4]) {
+#pragma unroll
+  for (int f = 0; f < 8; ++f) mine[64 * f + lane] = __builtin_bit_cast(u32x4, kf[f >> 2][f & 3]);
+  __syncthreads();
+#pragma unroll
+  for (int f = 0; f < 8; ++f) kf[2 + (f >> 2)][f & 3] = __builtin_bit_cast(bf16x8, partner[64 * f + lane]);
+  __syncthreads();
 }
 template <int NB = 4>
 __device__ __forceinline__ void chunk_gram_products(const bf16x8 (&kf)[4][4], f32x4 (&kk)[4][4]) {
@@ -1343,7 +1366,10 @@ __global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
       b_t[e] = e < ne ? bf2f(b[gi + e]) : 0.0f;
     }
     bf16x8 kf[4][4];
-    chunk_gram_loads(k, t0, c, hq, lane, kf);
+    if constexpr (pair_items)
+      chunk_gram_loads(k, t0, c, hq, lane, kf);
+    else
+      chunk_gram_loads<4, 2>(k, t0, c, hq, lane, kf, 2 * e0);
 
     const int h0 = kGva * hq + e0;
     float alog[kGva], dtb[kGva];
@@ -1368,6 +1394,9 @@ __global__ __launch_bounds__(kPrepassThreads, kGroups) void prepass_kernel(
     } else {
       float last[1];
       prepass_gates<1>(ws, c, a_t, b_t, alog, dtb, gp0, last);
+      auto* mine = reinterpret_cast<u32x4*>(&ws.nt[0][0][0][0]);
+      const auto* partner = reinterpret_cast<const u32x4*>(&sm.u.w[wv ^ 1].nt[0][0][0][0]);
+      trade_gram_halves(mine, partner, lane, kf);
       chunk_gram_products(kf, kk);
       prepass_terms<1, 0>(ws, kk, c, last, frag0, gp0);
     }
