@@ -1210,9 +1210,11 @@ __device__ __forceinline__ void chunk_gram_loads(const uint16_t* __restrict__ k,
 // through LDS into slots 2 and 3.  The exchange area is the wave's N-block
 // area (8 KB, unused until the terms), fragment f = 4 slot + m at
 // 16 (64 f + lane).  Two work-group barriers: the halves written, then read
-// (before any terms overwrite them).  Every wave of the group takes part: a
-// pair's items exist together (items come 8 per record), and waves without an
-// item have ended.
+// (before any terms overwrite them).  Every wave of the group takes part: in
+// each pass of the item loop the group's four waves hold items 4i .. 4i + 3
+// and the item count is a multiple of 8 (8 per record), so either all four
+// have an item or none has, and a wave that has ended no longer counts at a
+// barrier.
 static_assert(sizeof(PrepassWaveSmem::nt) >= 8 * 64 * sizeof(u32x4), "the exchange area holds eight fragments");
 __device__ __forceinline__ void trade_gram_halves(u32x4* mine, const u32x4* partner, int lane,
                                                   bf16x8 (&kf)[4][4]) {
