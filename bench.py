@@ -300,17 +300,21 @@ def planned_segment_chunks(ws, N, T, torch):
 
 def chain_step_us(args, torch, dev) -> dict:
     """Time of one chunk step of the consumer's sequential state chain: one
-    sequence of 4 chunks against one of 3 (warm cache; both too short to be
-    cut into segments and too long for the direct path, so the difference is
-    one chunk step of the chain)."""
+    sequence of 4 chunks against one of 3 (warm cache; too long for the direct
+    path, so the difference is one chunk step of the chain as long as the
+    planner cuts neither into segments, which it normally does not at these
+    lengths: `us` is None when it did)."""
     from kachua_mlsys_amd.inputs import prefill_inputs_from_lengths
 
-    t = {}
+    t, seg = {}, {}
     for nch in (3, 4):
         p = prefill_inputs_from_lengths([64 * nch], seed=11)
-        t[nch] = time_prefill(p, args, torch, dev, warm=True)["us_per_call"]
-    return {"us": round(t[4] - t[3], 3), "us_per_call_3_chunks": t[3], "us_per_call_4_chunks": t[4],
-            "method": "t(1 x 256 tokens) - t(1 x 192 tokens), warm cache"}
+        r = time_prefill(p, args, torch, dev, warm=True)
+        t[nch], seg[nch] = r["us_per_call"], r["segment_chunks"]
+    unsplit = all(seg[n] is None or seg[n] >= n for n in (3, 4))
+    return {"us": round(t[4] - t[3], 3) if unsplit else None, "us_per_call_3_chunks": t[3],
+            "us_per_call_4_chunks": t[4], "segment_chunks": [seg[3], seg[4]],
+            "method": "t(1 x 256 tokens) - t(1 x 192 tokens), warm cache, neither split"}
 
 
 # Prefill workloads beside the three configurations: configuration 3 with
@@ -514,7 +518,7 @@ def main():
             entry = time_prefill(p_cpu, args, torch, dev, traffic=f"prefill_c{cfg}_traffic.txt")
             if not args.warm_cache and not args.profile:
                 entry["us_per_call_warm"] = time_prefill(p_cpu, args, torch, dev, warm=True)["us_per_call"]
-            if cfg in (2, 3) and step is not None:
+            if cfg in (2, 3) and step is not None and step["us"] is not None:
                 # sequential floors: the longest sequence's chunks x chunk step
                 # without segments, and the longest run (at most L chunks) x
                 # step with the planner's segments (excluding the finish
