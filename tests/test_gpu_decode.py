@@ -135,3 +135,35 @@ def test_decode_torch_binding_path(gpu):
     # an argument outside the common case still gets the descriptive error
     with pytest.raises(TypeError, match="q: expected dtype"):
         decode.launch_gdn(d.q.float(), *d.args()[1:], out, ns)
+
+
+# Seeded random decode steps: batch size, wave shape, gate regime (default,
+# near-1 decay, strong decay with beta near 0 or 1), state magnitude, value
+# range and scale, all drawn from the seed; each step is compared with the
+# oracle at the usual bar.
+def _random_decode(seed):
+    gen = torch.Generator("cpu").manual_seed(20_000 + seed)
+    B = int(torch.randint(1, 97, (1,), generator=gen))
+    d = decode_inputs(B, seed=30_000 + seed)
+    regime = int(torch.randint(0, 4, (1,), generator=gen))
+    if regime == 1:     # near-1 decay
+        d.A_log = torch.empty(8).uniform_(-8.0, -5.0, generator=gen)
+    elif regime == 2:   # strong decay, beta close to 1
+        d.A_log = torch.empty(8).uniform_(1.0, 2.5, generator=gen)
+        d.b = d.b.float().add(6.0).to(torch.bfloat16)
+    elif regime == 3:   # beta close to 0
+        d.b = d.b.float().sub(8.0).to(torch.bfloat16)
+    d.state = d.state * float(10.0 ** torch.empty(1).uniform_(-2.0, 2.0, generator=gen))
+    d.v = (d.v.float() * float(10.0 ** torch.empty(1).uniform_(-1.0, 1.0, generator=gen))).to(torch.bfloat16)
+    d.scale = float(torch.empty(1).uniform_(0.05, 0.2, generator=gen))
+    rows = (0, 16, 32)[int(torch.randint(0, 3, (1,), generator=gen))]
+    return d, rows, f"random decode seed={seed}: B={B} regime={regime} rows={rows}"
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_decode_random_steps(gpu, seed):
+    d, rows, label = _random_decode(seed)
+    print(f"[case] {label}", flush=True)
+    o_ref, s_ref = decode_ref(*d.args())
+    out, ns = _run(d, gpu, rows_per_wave=rows)
+    assert_parity(out, ns, o_ref, s_ref, label)
